@@ -1,0 +1,204 @@
+"""Benchmark of the routed-MoE layer on one MI355X.
+
+A step is one MoE layer call (router GEMV + softmax top-k, grouped SwiGLU experts incl. the shared expert, gated
+combine) over one batch of T decode tokens whose activations are already resident in HBM.  Expert tables of
+`--layers` distinct layers are resident and the steps rotate over them, so the working set (4 GB per Solar layer)
+is far larger than the 256 MB Infinity Cache and every step streams its experts from HBM.
+
+Prints one JSON line.  value = microseconds per MoE layer per token (lower is better); the line also carries the
+achieved HBM bandwidth (algorithmic bytes / time) as a fraction of the 8 TB/s peak, the dominant kernel's roofline
+figure measured with hipEvents on the stream it runs on, and the reference CPU path timed on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "npu-offload_amd"))
+
+from moe_gpu import INT8, MoeGpu, synth_c, synth_key  # noqa: E402
+from moe_gpu.workloads import SOLAR, SOLAR_INT8, TINY, Workload, solar_batch, zipf_bias  # noqa: E402
+
+METRIC = "MoE layer µs/token + achieved HBM TB/s (fraction of ~8 TB/s), bf16 batch 1"
+HBM_PEAK_GBPS = 8000.0
+WORKLOADS = {"solar": SOLAR, "solar-int8": SOLAR_INT8, "solar-b2": solar_batch(2), "solar-b4": solar_batch(4),
+             "solar-b8": solar_batch(8), "tiny": TINY}
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w: Workload, budget_s: float = 12.0) -> dict | None:
+    """The reference's CPU expert path timed on this host: ck_gemv router + host route + ck_moe3 over the shared
+    expert and the routed experts (track2_opt/solar_engine/src/main.rs:128-141 `moe_host`), built from the
+    reference's own cpu_kern.c; falls back to the scalar restatement when AVX-512 BF16 is unavailable."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    H, F, E, k = w.H, w.F, w.E, w.k
+    cores = len(os.sched_getaffinity(0))
+    cores = int(os.environ.get("OMP_NUM_THREADS", cores))
+    ne = 48  # expert pool rotated beyond the LLC, as track2_opt/solar_engine/src/bin/cpu_bench.rs:15-31
+    n = F * H
+    src = O.f2bf((np.arange(3 * n) % 97).astype(np.float32) * 1e-4)
+    g, u, d = src[:n].reshape(F, H), src[n:2 * n].reshape(F, H), src[2 * n:].reshape(H, F)
+    x = O.f2bf((np.arange(H) % 13).astype(np.float32) * 0.01)
+    wr = O.f2bf(np.random.default_rng(0).normal(0, 0.02, (E, H)).astype(np.float32))
+    bias = zipf_bias(E, w.zipf_s, 0)
+    kind = "reference" if O.ref_available() else "port"
+    if kind == "reference":
+        R = O.Ref()
+        R.set_threads(cores)
+        pool = [R.place_expert(g, u, d) for _ in range(ne)]
+        gemv, moe3 = R.gemv, R.moe3
+    else:
+        cores = 1
+        pool = [np.concatenate([g.ravel(), u.ravel(), d.ravel()]) for _ in range(4)]
+        ne = len(pool)
+        gemv = O.gemv
+        moe3 = O.ck_moe3
+    keep = w.keep_eff
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    it = 0
+    while (it < 60 or time.perf_counter() < t_end) and it < 5000:
+        bases = [pool[(it * (keep + w.n_shared) + j) % ne] for j in range(keep + w.n_shared)]
+        t0 = time.perf_counter()
+        lg = gemv(wr, x)
+        ids, gates = O.route(lg, bias, k, keep)
+        out = np.zeros(H, np.float32)
+        if w.n_shared:
+            moe3(bases[keep:], np.ones(w.n_shared, np.float32), x, out, H, F)
+        moe3(bases[:keep], gates[0, :keep], x, out, H, F)
+        dt = time.perf_counter() - t0
+        if it >= 10:
+            ts.append(dt)
+        it += 1
+        if kind == "port" and it >= 3:
+            ts.append(dt)
+            break
+    med = statistics.median(ts)
+    nbytes = w.router_bytes() + (keep + w.n_shared) * 3 * F * H * 2
+    return {"value": round(med * 1e6, 1), "unit": "us/layer/token", "cores": cores, "kind": kind,
+            "GBps": round(nbytes / med / 1e9, 1),
+            "sample": f"{len(ts)} batch-1 layer calls (bf16, {keep} routed + {w.n_shared} shared experts from a "
+                      f"{ne}-expert pool + router GEMV/top-k), median; {'cpu_kern.c ck_gemv+ck_moe3' if kind == 'reference' else 'scalar restatement'}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the expert tier shards by expert across "
+              "GPUs only by design, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    w = WORKLOADS[args.workload]
+    T, L = w.T, args.layers
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"workload {w.name}: creating tier with {L} resident layers")
+    tier = MoeGpu(w.H, w.F, w.E, w.k, w.n_shared, n_layers=L, max_tokens=max(8, T))
+    stream = torch.cuda.Stream()  # a real stream handle (the current stream is the null stream), default priority
+    torch.cuda.set_stream(stream)
+    tier.set_stream(stream)
+    for l in range(L):
+        tier.synth_layer(l, 1000 + l, w.sigma_w, zipf_bias(w.E, w.zipf_s, 1000 + l))
+        if w.int8:
+            tier.quantize_layer(l)
+    flags = INT8 if w.int8 else 0
+    P = 64  # distinct token activations
+    xs = torch.empty((P, T, w.H), dtype=torch.int16, device=dev)
+    tier.synth_fill(xs, P * T * w.H, synth_key(7, 1 << 40), synth_c(1.0))
+    out = torch.empty((T, w.H), dtype=torch.float32, device=dev)
+    K, W = args.steps, args.warmup
+    ids = torch.empty((K, T, w.k), dtype=torch.int32, device=dev)
+    gates = torch.empty((K, T, w.k), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    log(f"warmup {W} steps")
+    for i in range(W):
+        tier.layer_dev(i % L, T, xs[i % P], out, ids[i % K], gates[i % K], keep=w.keep, flags=flags)
+    torch.cuda.synchronize()
+    log(f"timing {K} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        tier.layer_dev(i % L, T, xs[i % P], out, ids[i], gates[i], keep=w.keep, flags=flags)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_ms = e0.elapsed_time(e1)
+    ms_per_step = wall_ms / K
+    # algorithmic bytes: router + each distinct routed expert of the step once + shared experts
+    idh = ids.cpu().numpy()
+    keep = w.keep_eff
+    distinct = [len(set(idh[i, :, :keep].ravel().tolist())) for i in range(K)]
+    bytes_steps = [w.algorithmic_bytes(u) for u in distinct]
+    avg_bytes = float(np.mean(bytes_steps))
+    achieved = avg_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"{ms_per_step * 1e3:.2f} us/step (events {ev_ms / K * 1e3:.2f}), {achieved:.0f} GB/s algorithmic")
+
+    roofline = None
+    kernels = None
+    if not args.no_profile:
+        log("per-kernel event pass")
+        tier.profile_reset()
+        tier.profile_kernels(True)
+        for i in range(K):
+            tier.layer_dev(i % L, T, xs[i % P], out, ids[i], gates[i], keep=w.keep, flags=flags)
+        torch.cuda.synchronize()
+        prof = tier.profile_read()
+        tier.profile_kernels(False)
+        kernels = {n: {"avg_us": round(ms / max(c, 1) * 1e3, 2), "launches": c} for n, (ms, c) in prof.items() if c}
+        # dominant kernel: gate|up streams 2/3 of every expert's bytes
+        gu_ms, gu_n = prof["gateup_kernel"]
+        gu_avg_s = gu_ms / gu_n * 1e-3
+        per_expert_gu = 2 * w.F * w.H * (1 if w.int8 else 2)
+        gu_bytes = np.mean([u * per_expert_gu + w.n_shared * 2 * w.F * w.H * 2 for u in distinct])
+        gu_gbps = gu_bytes / gu_avg_s / 1e9
+        roofline = {"kernel": "gateup_kernel", "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "bytes_per_launch": int(gu_bytes)}
+
+    cpu = None
+    if not args.no_cpu_baseline and w.T == 1:
+        log("cpu baseline")
+        cpu = cpu_baseline(w)
+
+    us_tok = ms_per_step * 1e3 / T
+    line = {
+        "metric": METRIC, "value": round(us_tok, 2), "unit": "us/layer/token", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8w-bf16" if w.int8 else "bf16", "data": "synthetic (seeded, weights ~N(0,0.02), x ~N(0,1))",
+        "achieved_TBps": round(achieved / 1e3, 3), "hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes_per_step": int(avg_bytes), "event_ms_per_step": round(ev_ms / K, 5),
+        "decode_layer_calls_per_s": round(1e3 / ms_per_step, 1),
+        "config": {"workload": w.name, "H": w.H, "F": w.F, "E": w.E, "topk": w.k, "n_shared": w.n_shared,
+                   "tokens": T, "keep": keep, "resident_layers": L, "distinct_experts_avg": float(np.mean(distinct))},
+        "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
+    }
+    tier.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,147 @@
+/*
+ * moe_gpu.h — C ABI of the MI355X (gfx950) routed-MoE expert tier.
+ *
+ * The library replaces, for one GPU holding every expert of every layer in HBM, the expert tiers of
+ * npu-offload's Rust engine (track2_opt/solar_engine): the NPU expert kernels driven through chip.rs and the host
+ * CPU cold-expert path bound by the extern "C" block of track2_opt/solar_engine/src/host.rs:18-37 (compiled from
+ * track2_opt/solar_engine/csrc/cpu_kern.c).  Conventions follow that block:
+ *   - bf16 travels as raw uint16_t bits; int8 weights as int8_t; gates and outputs as fp32; dimensions are int.
+ *   - The caller owns every buffer it passes.  The library owns its HBM tables and per-call workspace.
+ *   - Unlike the void ck_* functions, every entry point returns MOE_GPU_OK (0) or a negative MOE_GPU_E* code and
+ *     keeps a message for moe_gpu_last_error() (the engine's chip replies are eyre::Result, chip.rs:59).
+ *   - A context is thread-affine: one host thread drives one context (the chip-thread pattern, chip.rs:96-143).
+ *
+ * Shapes: H hidden, F expert intermediate, E routed experts, k = topk, S = n_shared always-on experts, T tokens.
+ * Constraints: H % 512 == 0, H <= 16384, F % 256 == 0, E <= 512, 1 <= k <= 8, 0 <= S <= 4, 1 <= T <= max_tokens <= 16,
+ * max_tokens * H * 2 <= 96 KB (the tokens' activations are staged in LDS).
+ *
+ * Expert math (solar_hybrid/cpu_moe.cpp:38-96 semantics): for expert e and token t,
+ *   g = Wg_e x_t, u = Wu_e x_t (fp32 accumulation of bf16 products), act = bf16(silu(g) * u),
+ *   y_e[t] = Wd_e act (fp32).
+ * Routing (npu-kernels/.../layer_template/src/host.rs.tpl:247-267, softmax scoring): score = logits + bias; the k
+ * largest scores are selected (exact ties -> lower expert index); gates over the first `keep` ranks are the
+ * softmax restricted to them (renormalised); ranks >= keep are dropped (their gate is 0).
+ * Combine, per token, in this fixed order: out[t] (= 0, or the caller's value with MOE_GPU_ACCUMULATE)
+ *   += y_shared_s[t] for s = 0..S-1, then += gate[t,r] * y_{id[t,r]}[t] for r = 0..keep-1 (one fused multiply-add
+ *   per term).  A token's result does not depend on which other tokens share the call.
+ */
+#ifndef MOE_GPU_H
+#define MOE_GPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_gpu moe_gpu;
+
+enum {
+    MOE_GPU_OK = 0,
+    MOE_GPU_EINVAL = -1,   /* bad argument, shape or layer/expert index */
+    MOE_GPU_EHIP = -2,     /* HIP runtime error (message has hipGetErrorString) */
+    MOE_GPU_ENOMEM = -3,   /* HBM allocation failed */
+    MOE_GPU_ESTATE = -4,   /* weights not loaded for the requested layer / path */
+    MOE_GPU_ENOKERNEL = -5 /* the HIP code object for this GPU is missing (wrong arch) */
+};
+
+/* flags for the compute calls */
+#define MOE_GPU_ACCUMULATE 1u /* out += result (ck_* semantics, cpu_kern.c:141 `out[h] += ...`) instead of out = result */
+#define MOE_GPU_INT8 2u       /* routed experts use their int8 weight-only copy (ck_moe_q8w, cpu_kern.c:306-333) */
+
+/* ----------------------------------------------------------------------------------------------- context
+ * Replaces Chip::spawn (track2_opt/solar_engine/src/chip.rs:96-111) for a HIP device: creates the stream and the
+ * per-call workspace.  Layer tables are allocated on first load.  n_layers bounds the layer index. */
+int moe_gpu_create(int device, int H, int F, int E, int topk, int n_shared, int n_layers, int max_tokens,
+                   moe_gpu** out);
+void moe_gpu_destroy(moe_gpu* ctx);
+/* Message of the last failing call on this context (never NULL).  With ctx == NULL: the last create() failure. */
+const char* moe_gpu_last_error(const moe_gpu* ctx);
+/* Run subsequent work on `stream` (a hipStream_t, e.g. the caller's current stream); NULL restores the
+ * context's own stream. */
+int moe_gpu_set_stream(moe_gpu* ctx, void* stream);
+int moe_gpu_synchronize(moe_gpu* ctx);
+
+/* ----------------------------------------------------------------------------------------------- weights
+ * Host row-major bf16 -> HBM in the GPU layout.  Replaces the expert-table upload of chip.rs:208-233 and the
+ * NUMA placement ck_place_expert (cpu_kern.c:124-138, host.rs:144-153).  g, u: [F,H]; d: [H,F]. */
+int moe_gpu_load_expert(moe_gpu* ctx, int layer, int e, const uint16_t* g, const uint16_t* u, const uint16_t* d);
+/* Always-on shared expert s (gate 1.0): host's moe_cpu(&[sh], &[1.0]) at main.rs:131-135. */
+int moe_gpu_load_shared(moe_gpu* ctx, int layer, int s, const uint16_t* g, const uint16_t* u, const uint16_t* d);
+/* Router weight wr [E,H] bf16 (mlp.gate.weight, main.rs:129) and optional per-expert score bias [E] (NULL = 0). */
+int moe_gpu_load_router(moe_gpu* ctx, int layer, const uint16_t* wr, const float* bias);
+/* Device-pointer twins of the three loads (source already in HBM, e.g. a safetensors slab copied once). */
+int moe_gpu_load_expert_dev(moe_gpu* ctx, int layer, int e, const uint16_t* g, const uint16_t* u, const uint16_t* d);
+int moe_gpu_load_shared_dev(moe_gpu* ctx, int layer, int s, const uint16_t* g, const uint16_t* u, const uint16_t* d);
+/* int8 weight-only copy of routed expert e in ck_place_expert_q8's layout (cpu_kern.c:226-241):
+ * q = [(2F + H) rows] (gate rows, up rows: length H; then down rows: length F), sc = [2F + H] fp32 row scales. */
+int moe_gpu_load_expert_q8(moe_gpu* ctx, int layer, int e, const int8_t* q, const float* sc);
+/* Quantise the resident bf16 routed experts [e0, e1) of a layer on the device with quant_row's rule
+ * (cpu_kern.c:218-224: s = max|w|/127 or 1, q = rint(w * (1/s)) clamped to +-127); bit-identical to the host
+ * quantiser.  Replaces ck_place_expert_q8 at engine init (main.rs:509-516). */
+int moe_gpu_quantize_experts(moe_gpu* ctx, int layer, int e0, int e1);
+/* Read back the int8 copy of expert e in ck_place_expert_q8's layout (for checks). */
+int moe_gpu_get_expert_q8(moe_gpu* ctx, int layer, int e, int8_t* q, float* sc);
+
+/* ----------------------------------------------------------------------------------------------- compute (host buffers)
+ * Synchronous; x [T,H] bf16, out [T,H] fp32, ids/gates [T,k].  */
+
+/* Router GEMV + softmax top-k on the device: replaces ck_gemv(mlp.gate.weight) (cpu_kern.c:31-35, main.rs:129) or the
+ * NPU shared_router logits (dense/shared.rs:191-210) followed by the host route() (host.rs:119-128).  keep <= 0 means
+ * keep = k.  logits [T,E] may be NULL. */
+int moe_gpu_route(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, int32_t* ids, float* gates,
+                  float* logits);
+/* Grouped routed experts + shared experts + combine for caller-chosen ids/gates [T,k]: replaces ck_moe3
+ * (cpu_kern.c:141-172, via moe_cpu_placed host.rs:156-159), ck_moe_q8w (with MOE_GPU_INT8), the batched cpu_moe
+ * (cpu_moe.cpp:38-96) and the NPU ffn_k8/experts_b + combine kernels dispatched by moe_phase (main.rs:149-209).
+ * Ranks >= keep are skipped (keep <= 0: all k), and so is any rank whose id is -1 (a token may carry fewer experts
+ * than keep, as the variable-E ck_* calls do).  Gates are used as given (no renormalisation).
+ * with_shared = 0 leaves the shared experts out (the routed-only sum of ck_moe3). */
+int moe_gpu_moe(moe_gpu* ctx, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates, int keep,
+                int with_shared, unsigned flags, float* out);
+/* route + moe in one call, ids never leave the device (LayerA2 + ExpertsB of chip.rs combined).
+ * ids/gates may be NULL; when given they receive the routing decision. */
+int moe_gpu_layer(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, unsigned flags, float* out,
+                  int32_t* ids, float* gates);
+
+/* ----------------------------------------------------------------------------------------------- compute (device buffers)
+ * Same operations on device pointers, enqueued on the context's stream without synchronising. */
+int moe_gpu_route_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, int32_t* ids, float* gates,
+                      float* logits);
+int moe_gpu_moe_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates,
+                    int keep, int with_shared, unsigned flags, float* out);
+int moe_gpu_layer_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, unsigned flags, float* out,
+                      int32_t* ids, float* gates);
+
+/* ----------------------------------------------------------------------------------------------- bench/test support
+ * No reference counterpart.  Deterministic synthetic weights generated in HBM (no host upload), bit-identical to the
+ * host generator of the test suite: element i of tensor `tid` = bf16((float)(IrwinHall8(mix64 stream of key) - mean)
+ * * c), key = synth_key(seed, tid); tid = (layer * 4096 + e) * 4 + m, m = 0 gate, 1 up, 2 down (shared s: e = 4000+s;
+ * router: e = 4095, m = 0); i = row-major index in the logical matrix.  c = sigma / 53509.9... */
+int moe_gpu_synth_layer(moe_gpu* ctx, int layer, uint64_t seed, float c_weight, const float* bias);
+int moe_gpu_synth_fill(moe_gpu* ctx, uint16_t* dst_dev, uint64_t n, uint64_t key, uint64_t start, float c);
+uint64_t moe_gpu_synth_key(uint64_t seed, uint64_t tensor_id);
+/* Duration in ms of the last compute call's kernels when timing is enabled (hipEvents on the context stream). */
+int moe_gpu_enable_timing(moe_gpu* ctx, int on);
+int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
+/* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent cooperative kernel that
+ * walks router rows, top-k/grouping, gate|up tiles and down tiles with on-device dependency counters; 0 runs one
+ * kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in workgroups
+ * per CU (0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused launch. */
+#define MOE_GPU_OPT_FUSED 1
+#define MOE_GPU_OPT_WG_PER_CU 2
+#define MOE_GPU_OPT_LAST_GRID 3
+int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
+int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
+/* Per-kernel profiling: with on != 0 every kernel launched by the compute calls is bracketed by a hipEvent pair on the
+ * stream it runs on.  profile_read synchronises and returns, for kernel slot `kernel` (0 .. moe_gpu_profile_slots()-1),
+ * the summed duration and the launch count since the last reset, and its kernel symbol name. */
+int moe_gpu_profile_kernels(moe_gpu* ctx, int on);
+int moe_gpu_profile_slots(void);
+int moe_gpu_profile_read(moe_gpu* ctx, int kernel, double* total_ms, int* launches, const char** name);
+int moe_gpu_profile_reset(moe_gpu* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_GPU_H */

@@ -1,0 +1,123 @@
+// moe_kernels.h — device data layout and launch helpers shared by the HIP kernels and the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kTileRows = 64;      // rows per weight tile: one row per lane of a wavefront
+constexpr int kChunk = 8;          // bf16 elements per 16-byte chunk
+constexpr int kChunkQ8 = 16;       // int8 elements per 16-byte chunk
+constexpr int kWaves = 4;          // wavefronts per workgroup in the GEMV kernels
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxTokens = 16;     // tokens per call (T * topk <= 128 entries for the grouping unit)
+constexpr int kMaxTopk = 8;
+constexpr int kMaxShared = 4;
+constexpr int kMaxExperts = 512;
+constexpr int kMaxSlots = kMaxShared + kMaxTokens * kMaxTopk;
+
+// Per-call expert grouping, built on the device: slot s < n_shared is shared expert s (expert = -1 - s) over all
+// tokens; routed slots follow in first-seen order scanning tokens then ranks (solar_hybrid/runtime.py:344-347).
+struct Slots {
+    int nslot;
+    int err;  // 1: an id outside [-1, E); 2: an expert repeated within one token (device-side validation)
+    int pad_[2];
+    int expert[kMaxSlots];
+    int ntok[kMaxSlots];
+    int tok[kMaxSlots][kMaxTokens];
+    int rank[kMaxSlots][kMaxTokens];  // routed: rank of this expert in token tok's top-k; shared: -1
+};
+
+// Where a layer's weights live.  Routed expert e's bf16 gate|up table starts at gu + e * gu_stride (elements), its down
+// table at dn + e * dn_stride; shared expert s at sgu + s * gu_stride, sdn + s * dn_stride.  int8 copies: gu_q8 + e *
+// q8_gu_stride (bytes), dn_q8 + e * q8_dn_stride, scales sc_q8 + e * (2F + H) (gate|up rows in tile order, then down).
+struct LayerPtrs {
+    const uint16_t* wr;
+    const float* bias;
+    const uint16_t* gu;
+    const uint16_t* dn;
+    const uint16_t* sgu;
+    const uint16_t* sdn;
+    const int8_t* gu_q8;
+    const int8_t* dn_q8;
+    const float* sc_q8;
+};
+
+struct Dims {
+    int H, F, E, k, n_shared, max_t;
+    __host__ __device__ size_t gu_stride() const { return (size_t)2 * F * H; }
+    __host__ __device__ size_t dn_stride() const { return (size_t)H * F; }
+};
+
+// Tiled layouts (element offsets):
+//   gate|up bf16: [F/32 tiles][H/8 chunks][64 rows][8];   tile row i -> f = 32*tile + 8*(i/16) + i%8, up = (i/8)%2
+//   down bf16:    [H/64 tiles][F/8 chunks][64 rows][8];   tile row i -> h = 64*tile + i
+//   int8 twins use 16-element chunks: [F/32][H/16][64][16] and [H/64][F/16][64][16].
+__host__ __device__ inline int gu_row_f(int tile, int i) { return 32 * tile + 8 * (i >> 4) + (i & 7); }
+__host__ __device__ inline int gu_row_up(int i) { return (i >> 3) & 1; }
+
+constexpr int kMaxHTiles = 256;  // H <= 16384 (64-row down tiles)
+
+// Everything one expert pipeline call needs (device pointers).
+struct ExpertArgs {
+    LayerPtrs L;
+    Dims d;
+    int T, keep, n_shared, int8, accumulate;  // n_shared: shared experts summed in this call (0 or d.n_shared)
+    const uint16_t* x;                        // [T][H] bf16
+    float* out;                               // [T][H] fp32
+    int32_t* ids;                             // [T][k]
+    float* gates;                             // [T][k]
+    Slots* slots;
+    uint16_t* act;                            // [maxs][max_t][F] bf16
+    float* ypart;                             // [T][n_shared + k][H] fp32
+};
+
+// Dependency counters of the fused kernel (zero between launches; the last workgroup of a launch clears them).
+struct Sync {
+    unsigned router_done;
+    unsigned route_ready;
+    unsigned exit_count;
+    unsigned err;  // set when a bounded wait gave up (sticky until the host clears it)
+    unsigned gu_done[kMaxSlots];
+    unsigned d_done[kMaxHTiles];
+};
+
+struct FusedArgs {
+    ExpertArgs e;
+    float* logits;  // [T][E]
+    Sync* sync;
+    int nR;         // router units (0 when the caller gives ids)
+    int do_topk;
+    int maxs;       // slots the unit list covers: n_shared + max_t * k
+};
+
+size_t lds_bytes(int T, int NT, int H, int F);
+
+// ---- launch helpers (moe_kernels.hip) ---------------------------------------------------------------------------
+hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, float* logits, hipStream_t st);
+hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
+                             const float* logits, int32_t* ids, float* gates, Slots* slots, hipStream_t st);
+hipError_t launch_gateup(const ExpertArgs& a, hipStream_t st);
+hipError_t launch_down(const ExpertArgs& a, hipStream_t st);
+hipError_t launch_combine(const ExpertArgs& a, hipStream_t st);
+// wg_per_cu <= 0: as many workgroups per CU as fit; grid_out receives the grid size
+hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out);
+
+hipError_t launch_relayout_gu(const uint16_t* g, const uint16_t* u, int H, int F, uint16_t* dst, hipStream_t st);
+hipError_t launch_relayout_dn(const uint16_t* d, int H, int F, uint16_t* dst, hipStream_t st);
+hipError_t launch_relayout_q8(const int8_t* q, const float* sc, int H, int F, int8_t* gu_dst, int8_t* dn_dst,
+                              float* sc_dst, hipStream_t st);
+hipError_t launch_unlayout_q8(const int8_t* gu_src, const int8_t* dn_src, const float* sc_src, int H, int F, int8_t* q,
+                              float* sc, hipStream_t st);
+hipError_t launch_quantize(const uint16_t* gu, const uint16_t* dn, int H, int F, int n_exp, size_t gu_stride,
+                           size_t dn_stride, int8_t* gu_q8, int8_t* dn_q8, float* sc, hipStream_t st);
+hipError_t launch_synth_tiled(uint64_t key_g, uint64_t key_u, uint64_t key_d, float c, int H, int F, uint16_t* gu,
+                              uint16_t* dn, hipStream_t st);
+hipError_t launch_synth_fill(uint16_t* dst, uint64_t n, uint64_t key, uint64_t start, float c, hipStream_t st);
+
+uint64_t synth_key(uint64_t seed, uint64_t tensor_id);
+// Returns true when the code object holds kernels for the current device.
+bool kernels_available();
+
+}  // namespace moe

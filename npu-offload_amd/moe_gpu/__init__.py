@@ -1,0 +1,350 @@
+"""Python view of libmoe_gpu (the MI355X routed-MoE expert tier) through its C ABI (include/moe_gpu.h).
+
+Mirrors the reference's host-side interface for this path:
+
+* ``MoeGpu`` — one GPU tier holding every expert in HBM (the chip thread of track2_opt/solar_engine/src/chip.rs:96-143
+  with the NPU tables replaced by HIP tables).  Methods keep the reference's names and argument meaning:
+  ``place_expert`` / ``place_expert_q8`` (host.rs:145, :168), ``moe_placed`` (``moe_cpu_placed``, host.rs:156:
+  ``out += sum_e w_e * expert_e(x)``), ``moe_q8`` (``moe_cpu_q8`` with Q8_MODE=w, host.rs:181-188), ``route``
+  (router GEMV + softmax top-k, host.rs.tpl:247-267) and ``layer`` (route + experts + shared + combine).
+* ``gpu_moe`` — the ``cpu_moe(x, gus, ds, toks, ws)`` operator of solar_hybrid/cpu_moe.cpp:38-96 (called from
+  runtime.py:325-328), with experts named by id on a ``MoeGpu`` instead of passed as host tensors.
+
+Errors surface as ``MoeGpuError`` carrying the library's code and message (the engine's eyre::Result replies).
+There is no CPU fallback: if libmoe_gpu.so is missing or has no code object for the GPU, construction raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Sequence
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libmoe_gpu.so")
+
+OK, EINVAL, EHIP, ENOMEM, ESTATE, ENOKERNEL = 0, -1, -2, -3, -4, -5
+ACCUMULATE, INT8 = 1, 2
+
+# exported symbols, in include/moe_gpu.h order
+SYMBOLS = (
+    "moe_gpu_create", "moe_gpu_destroy", "moe_gpu_last_error", "moe_gpu_set_stream", "moe_gpu_synchronize",
+    "moe_gpu_load_expert", "moe_gpu_load_shared", "moe_gpu_load_router", "moe_gpu_load_expert_dev",
+    "moe_gpu_load_shared_dev", "moe_gpu_load_expert_q8", "moe_gpu_quantize_experts", "moe_gpu_get_expert_q8",
+    "moe_gpu_route", "moe_gpu_moe", "moe_gpu_layer", "moe_gpu_route_dev", "moe_gpu_moe_dev", "moe_gpu_layer_dev",
+    "moe_gpu_synth_layer", "moe_gpu_synth_fill", "moe_gpu_synth_key", "moe_gpu_enable_timing", "moe_gpu_last_time_ms",
+    "moe_gpu_set_option", "moe_gpu_get_option",
+    "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
+)
+OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID = 1, 2, 3
+
+_lib = None
+
+
+class MoeGpuError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"moe_gpu error {code}: {msg}")
+        self.code = code
+
+
+def _bind_hip_runtime() -> None:
+    """A process must hold exactly one HIP runtime.  PyTorch wheels bundle their own libamdhip64 (same SONAME
+    libamdhip64.so.7, loaded by file name from torch/lib); if libmoe_gpu bound /opt/rocm's copy first, a later
+    `import torch` would load a second runtime that sees no GPU.  When torch is installed, load its copy first so
+    libmoe_gpu's libamdhip64.so.7 dependency resolves to it and both share devices, streams and memory."""
+    import importlib.util
+
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        spec = None
+    if spec is not None and spec.origin:
+        p = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
+        if os.path.exists(p):
+            C.CDLL(p, mode=C.RTLD_GLOBAL)
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Load libmoe_gpu.so (no compute happens here; safe without a GPU)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: build it with `python npu-offload_amd/build.py`")
+    _bind_hip_runtime()
+    L = C.CDLL(path)
+    vp, i, u, f = C.c_void_p, C.c_int, C.c_uint, C.c_float
+    sig = {
+        "moe_gpu_create": (i, [i, i, i, i, i, i, i, i, C.POINTER(vp)]),
+        "moe_gpu_destroy": (None, [vp]),
+        "moe_gpu_last_error": (C.c_char_p, [vp]),
+        "moe_gpu_set_stream": (i, [vp, vp]),
+        "moe_gpu_synchronize": (i, [vp]),
+        "moe_gpu_load_expert": (i, [vp, i, i, vp, vp, vp]),
+        "moe_gpu_load_shared": (i, [vp, i, i, vp, vp, vp]),
+        "moe_gpu_load_router": (i, [vp, i, vp, vp]),
+        "moe_gpu_load_expert_dev": (i, [vp, i, i, vp, vp, vp]),
+        "moe_gpu_load_shared_dev": (i, [vp, i, i, vp, vp, vp]),
+        "moe_gpu_load_expert_q8": (i, [vp, i, i, vp, vp]),
+        "moe_gpu_quantize_experts": (i, [vp, i, i, i]),
+        "moe_gpu_get_expert_q8": (i, [vp, i, i, vp, vp]),
+        "moe_gpu_route": (i, [vp, i, i, vp, i, vp, vp, vp]),
+        "moe_gpu_moe": (i, [vp, i, i, vp, vp, vp, i, i, u, vp]),
+        "moe_gpu_layer": (i, [vp, i, i, vp, i, u, vp, vp, vp]),
+        "moe_gpu_route_dev": (i, [vp, i, i, vp, i, vp, vp, vp]),
+        "moe_gpu_moe_dev": (i, [vp, i, i, vp, vp, vp, i, i, u, vp]),
+        "moe_gpu_layer_dev": (i, [vp, i, i, vp, i, u, vp, vp, vp]),
+        "moe_gpu_synth_layer": (i, [vp, i, C.c_uint64, f, vp]),
+        "moe_gpu_synth_fill": (i, [vp, vp, C.c_uint64, C.c_uint64, C.c_uint64, f]),
+        "moe_gpu_synth_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "moe_gpu_enable_timing": (i, [vp, i]),
+        "moe_gpu_last_time_ms": (i, [vp, C.POINTER(f)]),
+        "moe_gpu_set_option": (i, [vp, i, i]),
+        "moe_gpu_get_option": (i, [vp, i, C.POINTER(i)]),
+        "moe_gpu_profile_kernels": (i, [vp, i]),
+        "moe_gpu_profile_slots": (i, []),
+        "moe_gpu_profile_read": (i, [vp, i, C.POINTER(C.c_double), C.POINTER(i), C.POINTER(C.c_char_p)]),
+        "moe_gpu_profile_reset": (i, [vp]),
+    }
+    for name in SYMBOLS:
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = sig[name]
+    _lib = L
+    return L
+
+
+def _p(a) -> int | None:
+    """Pointer of a numpy array, a torch tensor or an int address."""
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if isinstance(a, np.ndarray):
+        assert a.flags.c_contiguous
+        return a.ctypes.data
+    if hasattr(a, "data_ptr"):
+        assert a.is_contiguous()
+        return a.data_ptr()
+    raise TypeError(type(a))
+
+
+def _u16(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    assert a.dtype == np.uint16, a.dtype
+    return a
+
+
+def synth_key(seed: int, tensor_id: int) -> int:
+    return int(load_library().moe_gpu_synth_key(seed, tensor_id))
+
+
+def tensor_id(layer: int, e: int, m: int) -> int:
+    """Synthetic tensor ids: routed e, shared s -> e = 4000 + s, router -> e = 4095 (m = 0 gate, 1 up, 2 down)."""
+    return (layer * 4096 + e) * 4 + m
+
+
+SYNTH_SD = float(np.sqrt(8 * (65536.0 ** 2 - 1) / 12))  # sd of the Irwin-Hall(8) integer sum
+
+
+def synth_c(sigma: float) -> float:
+    return float(np.float32(sigma / SYNTH_SD))
+
+
+class MoeGpu:
+    """One MI355X expert tier: every routed and shared expert of `n_layers` layers resident in HBM."""
+
+    def __init__(self, H: int, F: int, E: int, topk: int, n_shared: int = 0, n_layers: int = 1, max_tokens: int = 8,
+                 device: int = 0):
+        self.L = load_library()
+        h = C.c_void_p()
+        rc = self.L.moe_gpu_create(device, H, F, E, topk, n_shared, n_layers, max_tokens, C.byref(h))
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_gpu_last_error(None).decode())
+        self.h = h
+        self.H, self.F, self.E, self.k, self.n_shared, self.n_layers, self.max_tokens = (
+            H, F, E, topk, n_shared, n_layers, max_tokens)
+
+    # -------------------------------------------------------------------------------------------------- plumbing
+    def _chk(self, rc: int):
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_gpu_last_error(self.h).decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.moe_gpu_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream) -> None:
+        """stream: a torch.cuda.Stream, a raw hipStream_t address or None (the context's own stream).
+        A handle of 0 (the legacy null stream) also selects the context's own stream."""
+        s = getattr(stream, "cuda_stream", stream)
+        self._chk(self.L.moe_gpu_set_stream(self.h, s))
+
+    def synchronize(self):
+        self._chk(self.L.moe_gpu_synchronize(self.h))
+
+    def enable_timing(self, on: bool = True):
+        self._chk(self.L.moe_gpu_enable_timing(self.h, 1 if on else 0))
+
+    def last_time_ms(self) -> float:
+        v = C.c_float()
+        self._chk(self.L.moe_gpu_last_time_ms(self.h, C.byref(v)))
+        return float(v.value)
+
+    def set_option(self, opt: int, value: int):
+        self._chk(self.L.moe_gpu_set_option(self.h, opt, int(value)))
+
+    def get_option(self, opt: int) -> int:
+        v = C.c_int()
+        self._chk(self.L.moe_gpu_get_option(self.h, opt, C.byref(v)))
+        return int(v.value)
+
+    def profile_kernels(self, on: bool = True):
+        self._chk(self.L.moe_gpu_profile_kernels(self.h, 1 if on else 0))
+
+    def profile_reset(self):
+        self._chk(self.L.moe_gpu_profile_reset(self.h))
+
+    def profile_read(self) -> dict:
+        """{kernel name: (total ms, launches)} since the last reset (synchronises)."""
+        res = {}
+        for k in range(self.L.moe_gpu_profile_slots()):
+            ms, n, nm = C.c_double(), C.c_int(), C.c_char_p()
+            self._chk(self.L.moe_gpu_profile_read(self.h, k, C.byref(ms), C.byref(n), C.byref(nm)))
+            res[nm.value.decode()] = (float(ms.value), int(n.value))
+        return res
+
+    # -------------------------------------------------------------------------------------------------- weights
+    def place_expert(self, layer: int, e: int, g, u, d):
+        """host.rs:145 place_expert / chip.rs:208-233 table upload: bf16 g,u [F,H], d [H,F] -> HBM tables."""
+        g, u, d = _u16(g), _u16(u), _u16(d)
+        assert g.shape == (self.F, self.H) and u.shape == (self.F, self.H) and d.shape == (self.H, self.F)
+        self._chk(self.L.moe_gpu_load_expert(self.h, layer, e, _p(g), _p(u), _p(d)))
+
+    def place_shared(self, layer: int, s: int, g, u, d):
+        g, u, d = _u16(g), _u16(u), _u16(d)
+        assert g.shape == (self.F, self.H) and u.shape == (self.F, self.H) and d.shape == (self.H, self.F)
+        self._chk(self.L.moe_gpu_load_shared(self.h, layer, s, _p(g), _p(u), _p(d)))
+
+    def place_router(self, layer: int, wr, bias=None):
+        wr = _u16(wr)
+        assert wr.shape == (self.E, self.H)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self._chk(self.L.moe_gpu_load_router(self.h, layer, _p(wr), _p(b)))
+
+    def place_expert_q8(self, layer: int, e: int, q=None, sc=None):
+        """host.rs:168 place_expert_q8: with q/sc (ck_place_expert_q8 layout) upload them, else quantise the
+        resident bf16 copy on the device (same quant_row bits)."""
+        if q is None:
+            self._chk(self.L.moe_gpu_quantize_experts(self.h, layer, e, e + 1))
+        else:
+            q = np.ascontiguousarray(q, np.int8); sc = np.ascontiguousarray(sc, np.float32)
+            assert q.size == 3 * self.F * self.H and sc.size == 2 * self.F + self.H
+            self._chk(self.L.moe_gpu_load_expert_q8(self.h, layer, e, _p(q), _p(sc)))
+
+    def quantize_layer(self, layer: int, e0: int = 0, e1: int | None = None):
+        self._chk(self.L.moe_gpu_quantize_experts(self.h, layer, e0, self.E if e1 is None else e1))
+
+    def get_expert_q8(self, layer: int, e: int):
+        q = np.zeros(3 * self.F * self.H, np.int8); sc = np.zeros(2 * self.F + self.H, np.float32)
+        self._chk(self.L.moe_gpu_get_expert_q8(self.h, layer, e, _p(q), _p(sc)))
+        return q, sc
+
+    def synth_layer(self, layer: int, seed: int, sigma: float = 0.02, bias=None):
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self._chk(self.L.moe_gpu_synth_layer(self.h, layer, seed, synth_c(sigma), _p(b)))
+
+    def synth_fill(self, dst, n: int, key: int, c: float, start: int = 0):
+        self._chk(self.L.moe_gpu_synth_fill(self.h, _p(dst), n, key, start, c))
+
+    # -------------------------------------------------------------------------------------------------- compute (host)
+    def route(self, layer: int, x, keep: int = 0, want_logits: bool = False):
+        x = _u16(np.atleast_2d(x)); T = x.shape[0]
+        ids = np.zeros((T, self.k), np.int32); gates = np.zeros((T, self.k), np.float32)
+        lg = np.zeros((T, self.E), np.float32) if want_logits else None
+        self._chk(self.L.moe_gpu_route(self.h, layer, T, _p(x), keep, _p(ids), _p(gates), _p(lg)))
+        return (ids, gates, lg) if want_logits else (ids, gates)
+
+    def moe(self, layer: int, x, ids, gates, keep: int = 0, with_shared: bool = True, flags: int = 0, out=None):
+        x = _u16(np.atleast_2d(x)); T = x.shape[0]
+        ids = np.ascontiguousarray(np.atleast_2d(ids), np.int32); gates = np.ascontiguousarray(np.atleast_2d(gates), np.float32)
+        assert ids.shape == (T, self.k) and gates.shape == (T, self.k)
+        if out is None:
+            out = np.zeros((T, self.H), np.float32)
+        self._chk(self.L.moe_gpu_moe(self.h, layer, T, _p(x), _p(ids), _p(gates), keep, 1 if with_shared else 0, flags,
+                                     _p(out)))
+        return out
+
+    def layer(self, layer: int, x, keep: int = 0, flags: int = 0, out=None):
+        x = _u16(np.atleast_2d(x)); T = x.shape[0]
+        if out is None:
+            out = np.zeros((T, self.H), np.float32)
+        ids = np.zeros((T, self.k), np.int32); gates = np.zeros((T, self.k), np.float32)
+        self._chk(self.L.moe_gpu_layer(self.h, layer, T, _p(x), keep, flags, _p(out), _p(ids), _p(gates)))
+        return out, ids, gates
+
+    def moe_placed(self, layer: int, ids: Sequence[int], w, x, out: np.ndarray):
+        """moe_cpu_placed (host.rs:156 -> ck_moe3): out[H] += sum_e w[e] * expert_{ids[e]}(x), routed only."""
+        self._placed(layer, ids, w, x, out, 0)
+
+    def moe_q8(self, layer: int, ids: Sequence[int], w, x, out: np.ndarray):
+        """moe_cpu_q8 with Q8_MODE=w (host.rs:181-188 -> ck_moe_q8w): int8 weight-only routed experts, out +=."""
+        self._placed(layer, ids, w, x, out, INT8)
+
+    def _placed(self, layer, ids, w, x, out, flags):
+        n = len(ids)
+        if n == 0:
+            return
+        assert n <= self.k and out.dtype == np.float32 and out.size == self.H
+        idv = np.zeros((1, self.k), np.int32); gv = np.zeros((1, self.k), np.float32)
+        idv[0, :n] = ids; gv[0, :n] = w
+        o = out.reshape(1, self.H)
+        self._chk(self.L.moe_gpu_moe(self.h, layer, 1, _p(_u16(np.atleast_2d(x))), _p(idv), _p(gv), n, 0,
+                                     flags | ACCUMULATE, _p(o)))
+
+    # -------------------------------------------------------------------------------------------------- compute (device)
+    def layer_dev(self, layer: int, T: int, x, out, ids=None, gates=None, keep: int = 0, flags: int = 0):
+        self._chk(self.L.moe_gpu_layer_dev(self.h, layer, T, _p(x), keep, flags, _p(out), _p(ids), _p(gates)))
+
+    def moe_dev(self, layer: int, T: int, x, ids, gates, out, keep: int = 0, with_shared: bool = True, flags: int = 0):
+        self._chk(self.L.moe_gpu_moe_dev(self.h, layer, T, _p(x), _p(ids), _p(gates), keep, 1 if with_shared else 0,
+                                         flags, _p(out)))
+
+    def route_dev(self, layer: int, T: int, x, ids, gates, logits=None, keep: int = 0):
+        self._chk(self.L.moe_gpu_route_dev(self.h, layer, T, _p(x), keep, _p(ids), _p(gates), _p(logits)))
+
+
+def gpu_moe(tier: MoeGpu, layer: int, x, experts: Sequence[int], toks: Sequence, ws: Sequence) -> np.ndarray:
+    """cpu_moe (solar_hybrid/cpu_moe.cpp:38-96) on the GPU tier: experts by id, per-expert token rows and weights.
+
+    Returns out [T,H] fp32 = sum over experts (in list order, per token) of w * expert(x[tok]); no shared expert."""
+    x = _u16(np.atleast_2d(x)); T = x.shape[0]
+    per_tok: list[list] = [[] for _ in range(T)]
+    for e, tk, w in zip(experts, toks, ws):
+        for t, wt in zip(np.asarray(tk).tolist(), np.asarray(w, np.float32).tolist()):
+            per_tok[t].append((int(e), wt))
+    kmax = max((len(p) for p in per_tok), default=0)
+    if kmax > tier.k:
+        raise MoeGpuError(EINVAL, f"a token is routed to {kmax} experts > topk={tier.k}")
+    out = np.zeros((T, tier.H), np.float32)
+    if kmax == 0:
+        return out
+    # tokens with fewer experts leave their remaining ranks empty (id -1)
+    ids = np.full((T, tier.k), -1, np.int32); gates = np.zeros((T, tier.k), np.float32)
+    for t, p in enumerate(per_tok):
+        for r, (e, w) in enumerate(p):
+            ids[t, r], gates[t, r] = e, w
+    return tier.moe(layer, x, ids, gates, keep=kmax, with_shared=False)
