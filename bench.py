@@ -169,15 +169,20 @@ def main():
         prof = tier.profile_read()
         tier.profile_kernels(False)
         kernels = {n: {"avg_us": round(ms / max(c, 1) * 1e3, 2), "launches": c} for n, (ms, c) in prof.items() if c}
-        # dominant kernel: gate|up streams 2/3 of every expert's bytes
-        gu_ms, gu_n = prof["gateup_kernel"]
-        gu_avg_s = gu_ms / gu_n * 1e-3
-        per_expert_gu = 2 * w.F * w.H * (1 if w.int8 else 2)
-        gu_bytes = np.mean([u * per_expert_gu + w.n_shared * 2 * w.F * w.H * 2 for u in distinct])
-        gu_gbps = gu_bytes / gu_avg_s / 1e9
-        roofline = {"kernel": "gateup_kernel", "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS,
-                    "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                    "bytes_per_launch": int(gu_bytes)}
+        if prof.get("fused_layer_kernel", (0, 0))[1]:
+            # one fused kernel streams everything the layer reads: router, routed experts, shared expert
+            k_name, (k_ms, k_n) = "fused_layer_kernel", prof["fused_layer_kernel"]
+            k_bytes = avg_bytes
+        else:
+            # unfused: gate|up streams 2/3 of every expert's bytes and dominates
+            k_name, (k_ms, k_n) = "gateup_kernel", prof["gateup_kernel"]
+            per_expert_gu = 2 * w.F * w.H * (1 if w.int8 else 2)
+            k_bytes = float(np.mean([u * per_expert_gu + w.n_shared * 2 * w.F * w.H * 2 for u in distinct]))
+        k_avg_s = k_ms / k_n * 1e-3
+        k_gbps = k_bytes / k_avg_s / 1e9
+        roofline = {"kernel": k_name, "bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "bytes_per_launch": int(k_bytes), "avg_us": round(k_avg_s * 1e6, 2)}
 
     cpu = None
     if not args.no_cpu_baseline and w.T == 1:

@@ -125,7 +125,7 @@ uint64_t moe_gpu_synth_key(uint64_t seed, uint64_t tensor_id);
 int moe_gpu_enable_timing(moe_gpu* ctx, int on);
 int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 /* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent cooperative kernel that
- * walks router rows, top-k/grouping, gate|up tiles and down tiles with on-device dependency counters; 0 runs one
+ * walks router rows, top-k/grouping, gate|up tiles and down tiles (a work queue with on-device dependency counters); 0 runs one
  * kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in workgroups
  * per CU (0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused launch. */
 #define MOE_GPU_OPT_FUSED 1
@@ -133,6 +133,11 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 #define MOE_GPU_OPT_LAST_GRID 3
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
+/* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
+ * {start, dependencies met (0 if none), end, workgroup} in the 100 MHz s_memrealtime clock; read_trace copies the
+ * last launch's records (4 uint64 per unit, unit order: router rows, route, gate|up slot-major, down slot-major). */
+int moe_gpu_trace_units(moe_gpu* ctx, int on);
+int moe_gpu_read_trace(moe_gpu* ctx, uint64_t* buf, int max_units, int* units);
 /* Per-kernel profiling: with on != 0 every kernel launched by the compute calls is bracketed by a hipEvent pair on the
  * stream it runs on.  profile_read synchronises and returns, for kernel slot `kernel` (0 .. moe_gpu_profile_slots()-1),
  * the summed duration and the launch count since the last reset, and its kernel symbol name. */

@@ -64,6 +64,8 @@ struct moe_gpu {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     bool timing = false;
     bool timed = false;
+    uint64_t* d_trace = nullptr;  // fused-kernel unit trace (allocated when tracing is switched on)
+    int trace_units = 0;
     bool fused = true;     // one persistent kernel per layer call (MOE_GPU_OPT_FUSED)
     int wg_per_cu = 0;     // fused grid: workgroups per CU, 0 = as many as fit (MOE_GPU_OPT_WG_PER_CU)
     int last_grid = 0;
@@ -215,9 +217,9 @@ int end_timing(moe_gpu* c) {
     return MOE_GPU_OK;
 }
 
-enum { K_ROUTER = 0, K_TOPK = 1, K_GATEUP = 2, K_DOWN = 3, K_COMBINE = 4, K_FUSED = 5, K_SLOTS = 6 };
+enum { K_ROUTER = 0, K_TOPK = 1, K_GATEUP = 2, K_DOWN = 3, K_FUSED = 4, K_SLOTS = 5 };
 const char* const kKernelNames[K_SLOTS] = {"router_kernel", "topk_group_kernel", "gateup_kernel", "down_kernel",
-                                           "combine_kernel", "fused_layer_kernel"};
+                                           "fused_layer_kernel"};
 
 int prof_mark(moe_gpu* c, int kid) {  // called before and after each launch
     if (!c->profiling) return MOE_GPU_OK;
@@ -266,6 +268,7 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
     a.accumulate = (flags & MOE_GPU_ACCUMULATE) ? 1 : 0;
     a.x = x; a.out = out; a.ids = ids; a.gates = gates;
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
+    a.maxs = c->d.n_shared + T * keep;
     if (c->fused) {
         FusedArgs f;
         f.e = a;
@@ -273,16 +276,17 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
         f.sync = c->d_sync;
         f.nR = do_topk ? (c->d.E + moe::kWaves - 1) / moe::kWaves : 0;
         f.do_topk = do_topk ? 1 : 0;
-        f.maxs = c->d.n_shared + c->d.max_t * c->d.k;
+        f.trace = c->d_trace;
+        c->trace_units = f.nR + 1 + a.maxs * (c->d.F / 32) + a.maxs * (c->d.H / 64);
         LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->stream, &c->last_grid));
         return MOE_GPU_OK;
     }
     if (do_topk) LAUNCH(c, K_ROUTER, moe::launch_router(a.L, c->d, T, x, c->d_logits, c->stream));
-    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, n_shared, do_topk, c->d_logits, ids, gates,
+    // slots 0 .. d.n_shared-1 are always the shared experts' (summed only when this call includes them)
+    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, c->d.n_shared, do_topk, c->d_logits, ids, gates,
                                              c->d_slots, c->stream));
     LAUNCH(c, K_GATEUP, moe::launch_gateup(a, c->stream));
-    LAUNCH(c, K_DOWN, moe::launch_down(a, c->stream));
-    LAUNCH(c, K_COMBINE, moe::launch_combine(a, c->stream));
+    LAUNCH(c, K_DOWN, moe::launch_down(a, c->d_sync, c->stream));
     return MOE_GPU_OK;
 }
 
@@ -395,6 +399,7 @@ void moe_gpu_destroy(moe_gpu* c) {
     for (void* p : ws)
         if (p) (void)hipFree(p);
     for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
+    if (c->d_trace) (void)hipFree(c->d_trace);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
@@ -700,6 +705,34 @@ int moe_gpu_set_option(moe_gpu* c, int opt, int value) {
             return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
+}
+
+int moe_gpu_trace_units(moe_gpu* c, int on) {
+    int rc = enter(c);
+    if (rc) return rc;
+    if (on && !c->d_trace) {
+        const size_t units = (size_t)(c->d.E + moe::kWaves - 1) / moe::kWaves + 1 +
+                             (size_t)(c->d.n_shared + c->d.max_t * c->d.k) * (c->d.F / 32 + c->d.H / 64);
+        if ((rc = dev_alloc(c, (void**)&c->d_trace, units * 4 * sizeof(uint64_t), "unit trace"))) return rc;
+        HIPCHK(c, hipMemset(c->d_trace, 0, units * 4 * sizeof(uint64_t)));
+    } else if (!on && c->d_trace) {
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        HIPCHK(c, hipFree(c->d_trace));
+        c->d_trace = nullptr;
+    }
+    return MOE_GPU_OK;
+}
+
+int moe_gpu_read_trace(moe_gpu* c, uint64_t* buf, int max_units, int* units) {
+    int rc = enter(c);
+    if (rc) return rc;
+    if (!c->d_trace) return fail(c, MOE_GPU_ESTATE, "unit tracing is off");
+    if (!buf || !units) return fail(c, MOE_GPU_EINVAL, "NULL buffer");
+    const int n = c->trace_units < max_units ? c->trace_units : max_units;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(buf, c->d_trace, (size_t)n * 4 * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    *units = n;
+    return MOE_GPU_OK;
 }
 
 int moe_gpu_get_option(moe_gpu* c, int opt, int* value) {

@@ -64,6 +64,7 @@ struct ExpertArgs {
     LayerPtrs L;
     Dims d;
     int T, keep, n_shared, int8, accumulate;  // n_shared: shared experts summed in this call (0 or d.n_shared)
+    int maxs;                                 // slots this call can use: d.n_shared + T * keep
     const uint16_t* x;                        // [T][H] bf16
     float* out;                               // [T][H] fp32
     int32_t* ids;                             // [T][k]
@@ -74,34 +75,43 @@ struct ExpertArgs {
 };
 
 // Dependency counters of the fused kernel (zero between launches; the last workgroup of a launch clears them).
+// Every counter sits in its own 128-byte line so that pollers of one counter do not contend with another's.
+constexpr int kSyncPad = 32;  // unsigneds per counter
 struct Sync {
     unsigned router_done;
+    unsigned pad0_[kSyncPad - 1];
     unsigned route_ready;
+    unsigned pad1_[kSyncPad - 1];
     unsigned exit_count;
+    unsigned pad2_[kSyncPad - 1];
     unsigned err;  // set when a bounded wait gave up (sticky until the host clears it)
-    unsigned gu_done[kMaxSlots];
-    unsigned d_done[kMaxHTiles];
+    unsigned pad3_[kSyncPad - 1];
+    unsigned next_unit;  // work-queue head of the fused kernel
+    unsigned pad4_[kSyncPad - 1];
+    unsigned gu_done[kMaxSlots * kSyncPad];
+    unsigned d_done[kMaxHTiles * kSyncPad];
 };
 
 struct FusedArgs {
     ExpertArgs e;
     float* logits;  // [T][E]
     Sync* sync;
+    uint64_t* trace;  // optional: per unit {start, dependencies met, end, workgroup} in 100 MHz realtime ticks
     int nR;         // router units (0 when the caller gives ids)
     int do_topk;
-    int maxs;       // slots the unit list covers: n_shared + max_t * k
 };
 
-size_t lds_bytes(int T, int NT, int H, int F);
+size_t lds_bytes(int T, int NT, int H, int F, int E);
 
 // ---- launch helpers (moe_kernels.hip) ---------------------------------------------------------------------------
 hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, float* logits, hipStream_t st);
 hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
                              const float* logits, int32_t* ids, float* gates, Slots* slots, hipStream_t st);
 hipError_t launch_gateup(const ExpertArgs& a, hipStream_t st);
-hipError_t launch_down(const ExpertArgs& a, hipStream_t st);
-hipError_t launch_combine(const ExpertArgs& a, hipStream_t st);
-// wg_per_cu <= 0: as many workgroups per CU as fit; grid_out receives the grid size
+// down projection + the gated combine (the last down unit of each 64-row tile combines it)
+hipError_t launch_down(const ExpertArgs& a, Sync* sync, hipStream_t st);
+// wg_per_cu <= 0: as many workgroups per CU as fit (a plain launch: the work queue needs no co-residency);
+// grid_out receives the grid size
 hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out);
 
 hipError_t launch_relayout_gu(const uint16_t* g, const uint16_t* u, int H, int F, uint16_t* dst, hipStream_t st);

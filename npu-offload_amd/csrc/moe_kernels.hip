@@ -23,10 +23,11 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 // LDS pointers carry their address space so that reads compile to ds_read (LGKM counter), never to flat loads that
 // would share the vector-memory counter with the in-flight weight stream.
 #define LDS_AS __attribute__((address_space(3)))
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef LDS_AS u32x4 lds_u32x4;
 typedef LDS_AS float lds_float;
 
-constexpr unsigned kSpinLimit = 1u << 22;  // bounded dependency waits (~seconds): a wait never hangs the GPU
+constexpr unsigned kSpinLimit = 1u << 20;  // bounded dependency waits (~1 s): a wait never hangs the GPU
 
 __device__ __forceinline__ float bf_lo(unsigned v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf_hi(unsigned v) { return __uint_as_float(v & 0xFFFF0000u); }
@@ -54,6 +55,18 @@ __device__ __forceinline__ void unpack16_i8(const u32x4 v, float* f) {
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.f + expf(-g))) * u; }
 
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
+
+// Data that crosses workgroups inside one launch (logits, the slot table, ids/gates, act, partial outputs) is written
+// and read with agent-scope relaxed atomics: on gfx950 these are plain global loads/stores carrying the sc1 bit, which
+// keeps them coherent across the XCDs' L2s without any cache writeback or invalidate.  A producer orders its data
+// before the counter it bumps by waiting for its own stores to complete (vmcnt(0)) before the workgroup barrier; a
+// consumer reads the data only after it has observed the counter.  Agent-scope fences (an L2 writeback/invalidate per
+// wavefront, microseconds each under load) are never needed on the hot path.
+template <typename V>
+__device__ __forceinline__ V ld_sync(const V* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <typename V>
+__device__ __forceinline__ void st_sync(V* p, V v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void wait_own_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0), others untouched
 
 // wavefront index within the workgroup as a wave-uniform (scalar) value, so loop bounds derived from it stay scalar
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -188,17 +201,23 @@ struct Lds {
     lds_float* red;
 };
 
-size_t lds_bytes(int T, int NT, int H, int F) {
-    return (size_t)T * (H / 8) * 16 + (size_t)NT * (F / 8) * 16 + (size_t)4 * NT * 64 * 4;
+// `as` doubles as the route unit's score table: NT tokens x E (rounded up to 4) biased scores + NT x topk ranks.
+__host__ __device__ inline size_t as_bytes(int NT, int F, int E) {
+    const size_t act = (size_t)NT * (F / 8) * 16, route = (size_t)NT * (((E + 3) & ~3) + kMaxTopk) * 4;
+    return ((act > route ? act : route) + 15) & ~(size_t)15;
 }
 
-__device__ inline Lds lds_carve(unsigned char* base_generic, int T, int NT, int H, int F) {
+size_t lds_bytes(int T, int NT, int H, int F, int E) {
+    return (size_t)T * (H / 8) * 16 + as_bytes(NT, F, E) + (size_t)4 * NT * 64 * 4;
+}
+
+__device__ inline Lds lds_carve(unsigned char* base_generic, int T, int NT, int H, int F, int E) {
     LDS_AS unsigned char* base = (LDS_AS unsigned char*)base_generic;
     Lds s;
     s.xs = (lds_u32x4*)base;
     base += (size_t)T * (H / 8) * 16;
     s.as = (lds_u32x4*)base;
-    base += (size_t)NT * (F / 8) * 16;
+    base += as_bytes(NT, F, E);
     s.red = (lds_float*)base;
     return s;
 }
@@ -215,7 +234,7 @@ __device__ inline void stage_x(const Lds& s, const uint16_t* __restrict__ x, int
 // for bit by the host oracle): lane l owns chunks c = l + 64 j; per token a fused multiply-add chain over j
 // ascending and elements 0..7 ascending; then a 64-lane xor butterfly (32, 16, 8, 4, 2, 1).
 template <int NT>
-__device__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
+__device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
                             float* __restrict__ logits) {
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int e = e0 + wave;
@@ -254,7 +273,7 @@ __device__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e
             float v = acc[t];
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            if (lane == 0) logits[(size_t)t * E + e] = v;
+            if (lane == 0) st_sync(&logits[(size_t)t * E + e], v);
         }
     }
 }
@@ -263,124 +282,178 @@ __device__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e
 // Unit: softmax top-k (one wavefront per token, tokens strided over the 4 waves) and expert grouping (workgroup).
 // Selection compares biased logits, ties to the lower expert index; gates = softmax restricted to the kept ranks.
 // Grouping: routed slots in first-seen order scanning tokens then ranks; shared slots first.
-__device__ void route_unit(const Lds& s, const float* __restrict__ logits, const float* __restrict__ bias, int T,
-                           int E, int k, int keep, int n_shared, int do_topk, int32_t* __restrict__ ids,
-                           float* __restrict__ gates, Slots* __restrict__ slots) {
+// Maximum over the 64 lanes of a wavefront: DPP exchanges within rows of 16 lanes, then the four row results.
+__device__ __forceinline__ float dpp_max_step(float v, int ctrl_id) {
+    int o;
+    switch (ctrl_id) {  // dpp_ctrl must be a compile-time constant
+        case 0: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+        case 1: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
+        case 2: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        default: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
+    }
+    return fmaxf(v, __int_as_float(o));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max_step(v, 0);
+    v = dpp_max_step(v, 1);
+    v = dpp_max_step(v, 2);
+    v = dpp_max_step(v, 3);  // every lane of a 16-lane row now holds the row maximum
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ void route_unit(const Lds& s, const float* __restrict__ logits, const float* __restrict__ bias,
+                                           int T, int E, int k, int keep, int n_shared, int do_topk,
+                                           int32_t* __restrict__ ids, float* __restrict__ gates,
+                                           Slots* __restrict__ slots) {
+    __shared__ int ent_e[kMaxTokens * kMaxTopk];       // expert of entry (t, r), r < keep; -1 = empty rank
     __shared__ int first_pos[kMaxExperts];
     __shared__ int slot_of[kMaxExperts];
-    __shared__ int ent_e[kMaxTokens * kMaxTopk];
     __shared__ int ent_flag[kMaxTokens * kMaxTopk];
-    const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
-    if (do_topk) {
-        for (int t = wave; t < T; t += kWaves) {
-            float sc[kMaxExperts / 64];
-            unsigned selmask = 0;
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; i++) {
-                const int e = lane + 64 * i;
-                sc[i] = e < E ? logits[(size_t)t * E + e] + (bias ? bias[e] : 0.f) : -INFINITY;
-            }
-            float sel_sc[kMaxTopk];
-            int sel_id[kMaxTopk];
-#pragma unroll
-            for (int r = 0; r < kMaxTopk; r++) {
-                if (r < k) {
-                    float bv = -INFINITY;
-                    int bi = 0x7FFFFFFF;
-#pragma unroll
-                    for (int i = 0; i < kMaxExperts / 64; i++) {
-                        const int e = lane + 64 * i;
-                        if (e < E && !((selmask >> i) & 1u)) {
-                            if (sc[i] > bv || (sc[i] == bv && e < bi)) { bv = sc[i]; bi = e; }
-                        }
-                    }
-#pragma unroll
-                    for (int m = 32; m >= 1; m >>= 1) {
-                        const float ov = __shfl_xor(bv, m, 64);
-                        const int oi = __shfl_xor(bi, m, 64);
-                        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-                    }
-                    if (bi == 0x7FFFFFFF) bi = 0;  // only reachable with NaN scores
-                    if ((bi & 63) == lane) selmask |= 1u << (bi >> 6);
-                    sel_sc[r] = bv;
-                    sel_id[r] = bi;
-                }
-            }
-            if (lane == 0) {
-                float ex[kMaxTopk], tot = 0.f;
-#pragma unroll
-                for (int r = 0; r < kMaxTopk; r++) {
-                    if (r < k) {
-                        ex[r] = expf(sel_sc[r] - sel_sc[0]);
-                        if (r < keep) tot += ex[r];
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < kMaxTopk; r++) {
-                    if (r < k) {
-                        ids[t * k + r] = sel_id[r];
-                        gates[t * k + r] = r < keep ? ex[r] / tot : 0.f;
-                        if (r < keep) ent_e[t * keep + r] = sel_id[r];
-                    }
-                }
-            }
-        }
-    }
-    for (int e = tid; e < E; e += blockDim.x) first_pos[e] = 0x7FFFFFFF;
-    if (tid == 0) slots->err = 0;
-    __syncthreads();
+    const int tid = threadIdx.x;
     const int n = T * keep;
-    int my_e = -1;  // -1: empty rank (caller-given ids may leave ranks unused)
-    if (tid < n) {
-        if (do_topk) {
-            my_e = ent_e[tid];
-        } else {
-            my_e = ids[(tid / keep) * k + tid % keep];
-            if (my_e < -1 || my_e >= E) {  // out of range: flag and drop the entry
-                slots->err = 1;
-                my_e = -1;
+    if (tid == 0) st_sync(&slots->err, 0);
+    __syncthreads();
+    if (do_topk) {
+        // One wavefront per token (tokens strided over the workgroup's wavefronts).  Lane l holds the biased scores
+        // of experts l + 64 i.  Each of the k rounds takes the maximum remaining score with a DPP reduction (no
+        // shared-memory round trips) and the lowest expert index holding it with ballots, i.e. the order is
+        // (score descending, index ascending); NaN scores rank last.
+        const int wave = wave_id(), lane = tid & 63;
+        const int nI = (E + 63) / 64;
+        for (int t0 = 0; t0 < T; t0 += kWaves) {
+            const int t = t0 + wave;
+            if (t < T) {
+                float sc[kMaxExperts / 64];
+#pragma unroll
+                for (int i = 0; i < kMaxExperts / 64; i++)  // every load issued before any use: one round trip
+                    sc[i] = ld_sync(&logits[(size_t)t * E + min(lane + 64 * i, E - 1)]);
+#pragma unroll
+                for (int i = 0; i < kMaxExperts / 64; i++) {
+                    const int e = lane + 64 * i;
+                    float v = sc[i] + (bias ? bias[min(e, E - 1)] : 0.f);
+                    if (!(v == v)) v = -INFINITY;
+                    sc[i] = e < E ? v : -INFINITY;
+                }
+                unsigned live = 0;  // bit i: element i of this lane is a real, not yet selected expert
+#pragma unroll
+                for (int i = 0; i < kMaxExperts / 64; i++)
+                    if (lane + 64 * i < E) live |= 1u << i;
+                float my_sc = 0.f;
+                int my_id = 0;
+                for (int r = 0; r < k; r++) {
+                    float lm = -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < kMaxExperts / 64; i++)
+                        if ((live >> i) & 1u) lm = fmaxf(lm, sc[i]);
+                    const float m = wave_max(lm);
+                    int id = -1;
+                    for (int i = 0; i < nI && id < 0; i++) {
+                        const unsigned long long hit = __ballot(((live >> i) & 1u) && sc[i] == m);
+                        if (hit) id = 64 * i + (__ffsll(hit) - 1);
+                    }
+                    if (id < 0) id = 0;  // unreachable: k <= E and every live score is comparable
+                    if ((id & 63) == lane) live &= ~(1u << (id >> 6));
+                    if (lane == r) { my_sc = m; my_id = id; }
+                }
+                // gates: softmax restricted to the kept ranks; lane r holds rank r, rank 0 the maximum
+                const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), 0));
+                const float ex = expf(my_sc - top);
+                float tot = 0.f;
+                for (int q = 0; q < keep; q++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), q));
+                if (lane < k) {
+                    st_sync(&ids[t * k + lane], (int32_t)my_id);
+                    st_sync(&gates[t * k + lane], lane < keep ? ex / tot : 0.f);
+                    if (lane < keep) ent_e[t * keep + lane] = my_id;
+                }
             }
+        }
+    } else {
+        for (int p = tid; p < n; p += blockDim.x) {
+            int e = ld_sync(&ids[(p / keep) * k + p % keep]);
+            if (e < -1 || e >= E) {  // out of range: flag and drop the entry
+                st_sync(&slots->err, 1);
+                e = -1;
+            }
+            ent_e[p] = e;
         }
     }
     __syncthreads();
-    if (tid < n) {
-        ent_e[tid] = my_e;
+    // 4. grouping: routed slots in first-seen order scanning tokens then ranks (runtime.py:344-347), after the
+    //    n_shared shared slots.  Up to 64 entries (every decode batch of T * keep <= 64) are grouped in wave 0's
+    //    registers: lane i holds entry i, readlane/ballot replace shared-memory round trips.
+    if (n <= 64) {
+        if (tid < 64) {
+            const int lane = tid;
+            const int my_e = lane < n ? ent_e[lane] : -1;
+            int cnt = 0, pos = 0, firstj = 64;
+            for (int j = 0; j < n; j++) {
+                const int ej = __builtin_amdgcn_readlane(my_e, j);
+                const bool m = my_e >= 0 && ej == my_e;
+                cnt += m;
+                pos += m && j < lane;
+                if (m && j < firstj) firstj = j;
+            }
+            const bool flag = my_e >= 0 && firstj == lane;
+            const unsigned long long mask = __ballot(flag);
+            const int slot = n_shared + (int)__popcll(mask & ((1ull << firstj) - 1ull));  // slot of my first occurrence
+            if (flag) {
+                st_sync(&slots->expert[slot], my_e);
+                st_sync(&slots->ntok[slot], cnt < T ? cnt : T);
+            }
+            if (my_e >= 0) {
+                if (pos < T) {
+                    st_sync(&slots->tok[slot][pos], lane / keep);
+                    st_sync(&slots->rank[slot][pos], lane % keep);
+                } else {
+                    st_sync(&slots->err, 2);  // an expert repeated within one token's ids
+                }
+            }
+            if (lane == 0) st_sync(&slots->nslot, n_shared + (int)__popcll(mask));
+        }
+    } else {
+        for (int e = tid; e < E; e += blockDim.x) first_pos[e] = 0x7FFFFFFF;
+        __syncthreads();
+        const int my_e = tid < n ? ent_e[tid] : -1;
         if (my_e >= 0) atomicMin(&first_pos[my_e], tid);
-    }
-    __syncthreads();
-    if (tid < n) ent_flag[tid] = my_e >= 0 && first_pos[my_e] == tid;
-    __syncthreads();
-    if (tid < n && ent_flag[tid]) {
-        int before = 0;
-        for (int j = 0; j < tid; j++) before += ent_flag[j];
-        const int sl = n_shared + before;
-        slot_of[my_e] = sl;
-        int cnt = 0;
-        for (int j = 0; j < n; j++) cnt += ent_e[j] == my_e;
-        slots->expert[sl] = my_e;
-        slots->ntok[sl] = cnt < T ? cnt : T;
-    }
-    __syncthreads();
-    if (tid < n && my_e >= 0) {
-        const int sl = slot_of[my_e];
-        int pos = 0;
-        for (int j = 0; j < tid; j++) pos += ent_e[j] == my_e;
-        if (pos < T) {
-            slots->tok[sl][pos] = tid / keep;
-            slots->rank[sl][pos] = tid % keep;
-        } else {
-            slots->err = 2;  // an expert repeated within one token's ids
+        __syncthreads();
+        if (tid < n) ent_flag[tid] = my_e >= 0 && first_pos[my_e] == tid;
+        __syncthreads();
+        if (tid < n && ent_flag[tid]) {
+            int before = 0;
+            for (int j = 0; j < tid; j++) before += ent_flag[j];
+            const int sl = n_shared + before;
+            slot_of[my_e] = sl;
+            int cnt = 0;
+            for (int j = 0; j < n; j++) cnt += ent_e[j] == my_e;
+            st_sync(&slots->expert[sl], my_e);
+            st_sync(&slots->ntok[sl], cnt < T ? cnt : T);
+        }
+        __syncthreads();
+        if (my_e >= 0) {
+            const int sl = slot_of[my_e];
+            int pos = 0;
+            for (int j = 0; j < tid; j++) pos += ent_e[j] == my_e;
+            if (pos < T) {
+                st_sync(&slots->tok[sl][pos], tid / keep);
+                st_sync(&slots->rank[sl][pos], tid % keep);
+            } else {
+                st_sync(&slots->err, 2);
+            }
+        }
+        if (tid == 0) {
+            int nf = 0;
+            for (int j = 0; j < n; j++) nf += ent_flag[j];
+            st_sync(&slots->nslot, n_shared + nf);
         }
     }
     if (tid < n_shared) {
-        slots->expert[tid] = -1 - tid;
-        slots->ntok[tid] = T;
-        for (int j = 0; j < T; j++) { slots->tok[tid][j] = j; slots->rank[tid][j] = -1; }
-    }
-    if (tid == 0) {
-        int nf = 0;
-        for (int j = 0; j < n; j++) nf += ent_flag[j];
-        slots->nslot = n_shared + nf;
+        st_sync(&slots->expert[tid], -1 - tid);
+        st_sync(&slots->ntok[tid], T);
+        for (int j = 0; j < T; j++) { st_sync(&slots->tok[tid][j], j); st_sync(&slots->rank[tid][j], -1); }
     }
     __syncthreads();
 }
@@ -389,7 +462,7 @@ __device__ void route_unit(const Lds& s, const float* __restrict__ logits, const
 // Unit: gate|up tile.  Slot s, 32 f values = one 64-row tile (32 gate rows + their 32 up rows) over K = H, the 4
 // wavefronts splitting K; act[s][j][f] = bf16(silu(g) * u) for the slot's tokens.
 template <int N>
-__device__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
+__device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = H / 8;
@@ -420,15 +493,18 @@ __device__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile,
             float v = s.red[j * 64 + lane];
             if (q8) v = v * scale;
             const float up = __shfl_down(v, 8, 64);  // gate row lane (bit 3 clear) meets its up row (lane + 8)
-            if (j < ntok && !gu_row_up(lane))
-                a.act[((size_t)sl * a.d.max_t + j) * F + gu_row_f(tile, lane)] = f2bf_dev(silu_mul(v, up));
+            const unsigned h = f2bf_dev(silu_mul(v, up));
+            const unsigned h_next = __shfl_down(h, 1, 64);  // f + 1 lives in the next lane
+            if (j < ntok && !gu_row_up(lane) && !(lane & 1))
+                st_sync(reinterpret_cast<unsigned*>(a.act + ((size_t)sl * a.d.max_t + j) * F + gu_row_f(tile, lane)),
+                        h | (h_next << 16));
         }
     }
     __syncthreads();  // s.red is reused by the next unit
 }
 
 template <int NT>
-__device__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
+__device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
     if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, e, ntok, tok);
     else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, e, ntok, tok);
     else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, e, ntok, tok);
@@ -439,13 +515,14 @@ __device__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile,
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
 // slot and n_shared + rank for a routed one.
 template <int N>
-__device__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
+__device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank) {
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = F / 8;
-    const u32x4* src = reinterpret_cast<const u32x4*>(a.act + (size_t)sl * a.d.max_t * F);
-    for (int i = threadIdx.x; i < ntok * nc; i += blockDim.x) s.as[i] = src[i];
+    const unsigned* src = reinterpret_cast<const unsigned*>(a.act + (size_t)sl * a.d.max_t * F);
+    LDS_AS unsigned* dst = (LDS_AS unsigned*)s.as;
+    for (int i = threadIdx.x; i < ntok * (F / 2); i += blockDim.x) dst[i] = ld_sync(src + i);
     __syncthreads();
     int xoff[N];
 #pragma unroll
@@ -477,7 +554,7 @@ __device__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int
                 const int q = e < 0 ? sl : a.d.n_shared + rank[j];
                 float y = s.red[j * 64 + lane];
                 if (q8) y = y * scale;
-                a.ypart[((size_t)tok[j] * kq + q) * H + h] = y;
+                st_sync(&a.ypart[((size_t)tok[j] * kq + q) * H + h], y);
             }
         }
     }
@@ -485,7 +562,7 @@ __device__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int
 }
 
 template <int NT>
-__device__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
+__device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank) {
     if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank);
     else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank);
@@ -499,10 +576,92 @@ __device__ __forceinline__ void combine_elem(const ExpertArgs& a, int t, int h) 
     const int H = a.d.H, k = a.d.k, kq = a.d.n_shared + a.d.k;
     const size_t o = (size_t)t * H + h;
     float acc = a.accumulate ? a.out[o] : 0.f;
-    for (int q = 0; q < a.n_shared; q++) acc = acc + a.ypart[((size_t)t * kq + q) * H + h];
+    for (int q = 0; q < a.n_shared; q++) acc = acc + ld_sync(&a.ypart[((size_t)t * kq + q) * H + h]);
     for (int r = 0; r < a.keep; r++)
-        if (a.ids[t * k + r] >= 0) acc = fmaf(a.gates[t * k + r], a.ypart[((size_t)t * kq + a.d.n_shared + r) * H + h], acc);
+        if (ld_sync(&a.ids[t * k + r]) >= 0)
+            acc = fmaf(ld_sync(&a.gates[t * k + r]), ld_sync(&a.ypart[((size_t)t * kq + a.d.n_shared + r) * H + h]), acc);
     a.out[o] = acc;
+}
+
+// Coherent snapshot of one slot of the table the route unit published.
+template <int NT>
+struct SlotView {
+    int expert, ntok;
+    int tok[NT], rank[NT];
+    __device__ __forceinline__ void load(const Slots* sp, int sl) {  // independent loads: one round trip
+        expert = ld_sync(&sp->expert[sl]);
+        ntok = ld_sync(&sp->ntok[sl]);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            tok[j] = ld_sync(&sp->tok[sl][j]);
+            rank[j] = ld_sync(&sp->rank[sl][j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+            if (j >= ntok) tok[j] = rank[j] = 0;  // entries past ntok are stale: keep indices in range
+    }
+};
+
+// Publish this workgroup's coherent stores, then count the unit as done.
+__device__ __forceinline__ void signal_add(unsigned* p, unsigned v) {
+    wait_own_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll with relaxed agent-scope loads; after the barrier the workgroup reads the producers' data with ld_sync.
+__device__ __forceinline__ void wait_ge(unsigned* p, unsigned target, unsigned* err, uint64_t* stamp = nullptr) {
+    if (threadIdx.x == 0) {
+        unsigned n = 0;
+        while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            __builtin_amdgcn_s_sleep(2);
+            ++n;
+            // give up after kSpinLimit polls, or at once when another wait of this launch already gave up
+            if (n > kSpinLimit || ((n & 255) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        if (stamp) *stamp = __builtin_amdgcn_s_memrealtime();
+    }
+    __syncthreads();
+}
+
+
+
+// After a down unit of tile ht (live or skipped), count it; the last of the tile's maxs units combines the tile.
+__device__ __forceinline__ void down_done_combine(const ExpertArgs& a, Sync* sy, int ht) {
+    __shared__ int s_last;
+    wait_own_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&sy->d_done[ht * kSyncPad], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.maxs - 1);
+    __syncthreads();
+    if (s_last)  // every down unit of this tile has published its partial outputs
+        for (int i = threadIdx.x; i < a.T * 64; i += blockDim.x) combine_elem(a, i / 64, ht * 64 + i % 64);
+    __syncthreads();
+}
+
+// At kernel exit the last workgroup clears the counters for the next launch on this context.
+__device__ __forceinline__ void exit_and_reset(Sync* sy) {
+    __shared__ int s_last;
+    wait_own_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&sy->exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x - 1;
+    __syncthreads();
+    if (s_last) {
+        for (int i = threadIdx.x; i < kMaxSlots; i += blockDim.x) st_sync(&sy->gu_done[i * kSyncPad], 0u);
+        for (int i = threadIdx.x; i < kMaxHTiles; i += blockDim.x) st_sync(&sy->d_done[i * kSyncPad], 0u);
+        if (threadIdx.x == 0) {
+            st_sync(&sy->router_done, 0u);
+            st_sync(&sy->route_ready, 0u);
+            st_sync(&sy->next_unit, 0u);
+            st_sync(&sy->exit_count, 0u);
+        }
+    }
 }
 
 // ====================================================================================================================
@@ -510,7 +669,7 @@ __device__ __forceinline__ void combine_elem(const ExpertArgs& a, int t, int h) 
 __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T, const uint16_t* __restrict__ x,
                                                      float* __restrict__ logits) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F);
+    const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
     stage_x(s, x, T, d.H);
     if (T <= 1) router_unit<1>(s, L.wr, blockIdx.x * kWaves, d.E, d.H, T, logits);
     else if (T <= 4) router_unit<4>(s, L.wr, blockIdx.x * kWaves, d.E, d.H, T, logits);
@@ -522,87 +681,77 @@ __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, in
                                                          int32_t* __restrict__ ids, float* __restrict__ gates,
                                                          Slots* __restrict__ slots) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, 0, 0, d.H, d.F);
+    const Lds s = lds_carve(lds_raw, 0, T, d.H, d.F, d.E);
     route_unit(s, logits, L.bias, T, d.E, d.k, keep, n_shared, do_topk, ids, gates, slots);
 }
 
 template <int NT>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F);
+    const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     const int ntile = a.d.F / 32;
     const int sl = blockIdx.x / ntile, tile = blockIdx.x % ntile;
-    const Slots* sp = a.slots;
-    if (sl >= sp->nslot) return;
+    if (sl >= ld_sync(&a.slots->nslot) || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
+    SlotView<NT> v;
+    v.load(a.slots, sl);
     stage_x(s, a.x, a.T, a.d.H);
-    gateup_unit<NT>(s, a, sl, tile, sp->expert[sl], sp->ntok[sl], sp->tok[sl]);
+    gateup_unit<NT>(s, a, sl, tile, v.expert, v.ntok, v.tok);
 }
 
 template <int NT>
-__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a, Sync* sy) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, 0, NT, a.d.H, a.d.F);
+    const Lds s = lds_carve(lds_raw, 0, NT, a.d.H, a.d.F, a.d.E);
     const int nht = a.d.H / 64;
     const int sl = blockIdx.x / nht, ht = blockIdx.x % nht;
-    const Slots* sp = a.slots;
-    if (sl >= sp->nslot) return;
-    down_unit<NT>(s, a, sl, ht, sp->expert[sl], sp->ntok[sl], sp->tok[sl], sp->rank[sl]);
+    if (sl < ld_sync(&a.slots->nslot) && (sl >= a.d.n_shared || sl < a.n_shared)) {  // else unused / left out
+        SlotView<NT> v;
+        v.load(a.slots, sl);
+        down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
+    }
+    down_done_combine(a, sy, ht);
+    exit_and_reset(sy);
 }
 
-__global__ __launch_bounds__(256) void combine_kernel(ExpertArgs a) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= a.T * a.d.H) return;
-    combine_elem(a, idx / a.d.H, idx % a.d.H);
-}
 
 // ====================================================================================================================
-// Fused path: one persistent cooperative kernel walks the unit list
+// Fused path: one persistent kernel walks the unit list
 //   [router units][route unit][shared gate|up][routed gate|up][down, slot-major]
-// in a static round-robin (unit u -> workgroup u mod G, ascending).  A unit waits only on units of smaller index and
-// every workgroup of the cooperative grid is resident, so the lowest unfinished unit can always run; every wait is
-// bounded by kSpinLimit.  The last down unit of each 64-row tile combines that tile; the last workgroup to finish
-// clears the counters for the next launch.
-__device__ __forceinline__ void signal_add(unsigned* p, unsigned v) {
-    __threadfence();  // every thread publishes its own stores (agent scope) before the workgroup signals
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void wait_ge(unsigned* p, unsigned target, unsigned* err) {
-    if (threadIdx.x == 0) {
-        unsigned n = 0;
-        while (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++n > kSpinLimit) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
-
+// through a work queue: a global counter hands out unit indices in ascending order, and each workgroup fetches its
+// next index while it works on the current one.  A unit waits only on units of smaller index; the smallest
+// unfinished unit is therefore always some running workgroup's current unit and can proceed, so the grid needs no
+// co-residency guarantee (a plain launch).  Every wait is also bounded by kSpinLimit.  The last down unit of each
+// 64-row tile combines that tile; the last workgroup to finish clears the counters for the next launch.
 template <int NT>
 __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const ExpertArgs& a = f.e;
-    const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F);
+    const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     Sync* sy = f.sync;
     const int H = a.d.H, F = a.d.F;
     const int ntile = F / 32, nht = H / 64;
-    const int maxs = f.maxs;
+    const int maxs = a.maxs;
     const int uR = f.nR, uRoute = uR + 1, uGUs = uRoute + a.d.n_shared * ntile, uGU = uRoute + maxs * ntile;
     const int uEnd = uGU + maxs * nht;
-    __shared__ int s_last;
-    stage_x(s, a.x, a.T, H);
-    for (int u = blockIdx.x; u < uEnd; u += gridDim.x) {
+    __shared__ int s_unit;
+    if (threadIdx.x == 0) s_unit = (int)__hip_atomic_fetch_add(&sy->next_unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    stage_x(s, a.x, a.T, H);  // ends with a barrier: s_unit is visible
+    uint64_t t_start = 0;
+    for (int u = s_unit; u < uEnd;) {
+        int next = 0;
+        if (threadIdx.x == 0) {  // fetch the next unit now; its latency hides behind this unit's work
+            next = (int)__hip_atomic_fetch_add(&sy->next_unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (f.trace) {
+                t_start = __builtin_amdgcn_s_memrealtime();
+                f.trace[(size_t)u * 4 + 1] = 0;
+            }
+        }
         if (u < uR) {
             router_unit<NT>(s, a.L.wr, u * kWaves, a.d.E, H, a.T, f.logits);
             signal_add(&sy->router_done, 1);
         } else if (u < uRoute) {
-            if (uR) wait_ge(&sy->router_done, (unsigned)uR, &sy->err);
-            route_unit(s, f.logits, a.L.bias, a.T, a.d.E, a.d.k, a.keep, a.n_shared, f.do_topk, a.ids, a.gates,
+            if (uR) wait_ge(&sy->router_done, (unsigned)uR, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
+            route_unit(s, f.logits, a.L.bias, a.T, a.d.E, a.d.k, a.keep, a.d.n_shared, f.do_topk, a.ids, a.gates,
                        a.slots);
             signal_add(&sy->route_ready, 1);
         } else if (u < uGU) {
@@ -615,49 +764,37 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                     gateup_unit<NT>(s, a, sl, tile, -1 - sl, a.T, tok);
                 }
             } else {
-                wait_ge(&sy->route_ready, 1, &sy->err);
-                const Slots* sp = a.slots;
-                if (sl < sp->nslot) gateup_unit<NT>(s, a, sl, tile, sp->expert[sl], sp->ntok[sl], sp->tok[sl]);
+                wait_ge(&sy->route_ready, 1, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
+                if (sl < ld_sync(&a.slots->nslot)) {
+                    SlotView<NT> v;
+                    v.load(a.slots, sl);
+                    gateup_unit<NT>(s, a, sl, tile, v.expert, v.ntok, v.tok);
+                }
             }
-            signal_add(&sy->gu_done[sl], 1);
+            signal_add(&sy->gu_done[sl * kSyncPad], 1);
         } else {
             const int sl = (u - uGU) / nht, ht = (u - uGU) % nht;
             wait_ge(&sy->route_ready, 1, &sy->err);
-            const Slots* sp = a.slots;
-            const bool live = sl < sp->nslot && (sl >= a.d.n_shared || sl < a.n_shared);
+            const bool live = sl < ld_sync(&a.slots->nslot) && (sl >= a.d.n_shared || sl < a.n_shared);
             if (live) {
-                wait_ge(&sy->gu_done[sl], (unsigned)ntile, &sy->err);
-                down_unit<NT>(s, a, sl, ht, sp->expert[sl], sp->ntok[sl], sp->tok[sl], sp->rank[sl]);
+                SlotView<NT> v;
+                v.load(a.slots, sl);
+                wait_ge(&sy->gu_done[sl * kSyncPad], (unsigned)ntile, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
+                down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
             }
-            __threadfence();
-            __syncthreads();
-            if (threadIdx.x == 0)
-                s_last = __hip_atomic_fetch_add(&sy->d_done[ht], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-                         (unsigned)(maxs - 1);
-            __syncthreads();
-            if (s_last) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-                for (int i = threadIdx.x; i < a.T * 64; i += blockDim.x) combine_elem(a, i / 64, ht * 64 + i % 64);
-            }
-            __syncthreads();
+            down_done_combine(a, sy, ht);
         }
-    }
-    // the last workgroup out clears the counters for the next launch on this context
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(&sy->exit_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-                 gridDim.x - 1;
-    __syncthreads();
-    if (s_last) {
-        for (int i = threadIdx.x; i < kMaxSlots; i += blockDim.x) sy->gu_done[i] = 0;
-        for (int i = threadIdx.x; i < kMaxHTiles; i += blockDim.x) sy->d_done[i] = 0;
-        if (threadIdx.x == 0) {
-            sy->router_done = 0;
-            sy->route_ready = 0;
-            sy->exit_count = 0;
+        if (f.trace && threadIdx.x == 0) {
+            f.trace[(size_t)u * 4 + 0] = t_start;
+            f.trace[(size_t)u * 4 + 2] = __builtin_amdgcn_s_memrealtime();
+            f.trace[(size_t)u * 4 + 3] = blockIdx.x;
         }
+        __syncthreads();  // the whole workgroup is done with unit u before s_unit changes
+        if (threadIdx.x == 0) s_unit = next;
+        __syncthreads();
+        u = s_unit;
     }
+    exit_and_reset(sy);
 }
 
 // --------------------------------------------------------------------------------------------------------------------
@@ -828,7 +965,7 @@ static hipError_t set_lds(const void* fn, size_t lds) {
 static int nt_bucket(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
 hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, float* logits, hipStream_t st) {
-    const size_t lds = lds_bytes(T, 1, d.H, d.F);
+    const size_t lds = lds_bytes(T, 1, d.H, d.F, d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&router_kernel), lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kWaves)), dim3(256), lds, st, L, d, T, x, logits);
@@ -837,7 +974,9 @@ hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_
 
 hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
                              const float* logits, int32_t* ids, float* gates, Slots* slots, hipStream_t st) {
-    const size_t lds = lds_bytes(0, 0, d.H, d.F);
+    const size_t lds = lds_bytes(0, T, d.H, d.F, d.E);
+    hipError_t e = set_lds(reinterpret_cast<const void*>(&topk_group_kernel), lds);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), lds, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, logits,
                        ids, gates, slots);
     return hipGetLastError();
@@ -845,8 +984,8 @@ hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep,
 
 template <int NT>
 static hipError_t gateup_nt(const ExpertArgs& ea, hipStream_t st) {
-    const int maxs = ea.d.n_shared + ea.d.max_t * ea.d.k;
-    const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F);
+    const int maxs = ea.maxs;
+    const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&gateup_kernel<NT>), lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gateup_kernel<NT>, dim3(maxs * (ea.d.F / 32)), dim3(256), lds, st, ea);
@@ -854,12 +993,11 @@ static hipError_t gateup_nt(const ExpertArgs& ea, hipStream_t st) {
 }
 
 template <int NT>
-static hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
-    const int maxs = ea.d.n_shared + ea.d.max_t * ea.d.k;
-    const size_t lds = lds_bytes(0, NT, ea.d.H, ea.d.F);
+static hipError_t down_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
+    const size_t lds = lds_bytes(0, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&down_kernel<NT>), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(down_kernel<NT>, dim3(maxs * (ea.d.H / 64)), dim3(256), lds, st, ea);
+    hipLaunchKernelGGL(down_kernel<NT>, dim3(ea.maxs * (ea.d.H / 64)), dim3(256), lds, st, ea, sy);
     return hipGetLastError();
 }
 
@@ -873,39 +1011,43 @@ hipError_t launch_gateup(const ExpertArgs& ea, hipStream_t st) {
     }
 }
 
-hipError_t launch_down(const ExpertArgs& ea, hipStream_t st) {
+hipError_t launch_down(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     switch (nt_bucket(ea.T)) {
-        case 1: return down_nt<1>(ea, st);
-        case 2: return down_nt<2>(ea, st);
-        case 4: return down_nt<4>(ea, st);
-        case 8: return down_nt<8>(ea, st);
-        default: return down_nt<16>(ea, st);
+        case 1: return down_nt<1>(ea, sy, st);
+        case 2: return down_nt<2>(ea, sy, st);
+        case 4: return down_nt<4>(ea, sy, st);
+        case 8: return down_nt<8>(ea, sy, st);
+        default: return down_nt<16>(ea, sy, st);
     }
 }
 
-hipError_t launch_combine(const ExpertArgs& ea, hipStream_t st) {
-    hipLaunchKernelGGL(combine_kernel, dim3(nblk((size_t)ea.T * ea.d.H, 256)), dim3(256), 0, st, ea);
-    return hipGetLastError();
-}
 
 template <int NT>
 static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
     const void* fn = reinterpret_cast<const void*>(&fused_layer_kernel<NT>);
-    const size_t lds = lds_bytes(f.e.T, NT, f.e.d.H, f.e.d.F);
-    hipError_t e = set_lds(fn, lds);
-    if (e != hipSuccess) return e;
-    int dev = 0, per_cu = 0, ncu = 0;
+    const size_t lds = lds_bytes(f.e.T, NT, f.e.d.H, f.e.d.F, f.e.d.E);
+    // occupancy per (device, LDS size), computed once: the launch itself stays a single host call
+    static thread_local int c_dev = -1, c_ncu = 0, c_per_cu = 0;
+    static thread_local size_t c_lds = 0;
+    hipError_t e;
+    int dev = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
-    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds)) != hipSuccess) return e;
+    if (dev != c_dev || lds != c_lds) {
+        if ((e = set_lds(fn, lds)) != hipSuccess) return e;
+        if ((e = hipDeviceGetAttribute(&c_ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&c_per_cu, fn, 256, lds)) != hipSuccess) return e;
+        c_dev = dev;
+        c_lds = lds;
+    }
+    int per_cu = c_per_cu, ncu = c_ncu;
     if (wg_per_cu > 0 && wg_per_cu < per_cu) per_cu = wg_per_cu;
     if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const int units = f.nR + 1 + f.maxs * (f.e.d.F / 32) + f.maxs * (f.e.d.H / 64);
+    const int units = f.nR + 1 + f.e.maxs * (f.e.d.F / 32) + f.e.maxs * (f.e.d.H / 64);
     int grid = ncu * per_cu;
     if (grid > units) grid = units;
     if (grid_out) *grid_out = grid;
-    void* args[] = {&f};
-    return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(256), args, (unsigned)lds, st);
+    hipLaunchKernelGGL(fused_layer_kernel<NT>, dim3(grid), dim3(256), lds, st, f);
+    return hipGetLastError();
 }
 
 hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out) {

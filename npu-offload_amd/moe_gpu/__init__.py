@@ -22,7 +22,7 @@ from typing import Sequence
 import numpy as np
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG, "lib", "libmoe_gpu.so")
+LIB_PATH = os.environ.get("MOE_GPU_LIB") or os.path.join(PKG, "lib", "libmoe_gpu.so")
 
 OK, EINVAL, EHIP, ENOMEM, ESTATE, ENOKERNEL = 0, -1, -2, -3, -4, -5
 ACCUMULATE, INT8 = 1, 2
@@ -34,7 +34,7 @@ SYMBOLS = (
     "moe_gpu_load_shared_dev", "moe_gpu_load_expert_q8", "moe_gpu_quantize_experts", "moe_gpu_get_expert_q8",
     "moe_gpu_route", "moe_gpu_moe", "moe_gpu_layer", "moe_gpu_route_dev", "moe_gpu_moe_dev", "moe_gpu_layer_dev",
     "moe_gpu_synth_layer", "moe_gpu_synth_fill", "moe_gpu_synth_key", "moe_gpu_enable_timing", "moe_gpu_last_time_ms",
-    "moe_gpu_set_option", "moe_gpu_get_option",
+    "moe_gpu_set_option", "moe_gpu_get_option", "moe_gpu_trace_units", "moe_gpu_read_trace",
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
 )
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID = 1, 2, 3
@@ -101,6 +101,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_gpu_enable_timing": (i, [vp, i]),
         "moe_gpu_last_time_ms": (i, [vp, C.POINTER(f)]),
         "moe_gpu_set_option": (i, [vp, i, i]),
+        "moe_gpu_trace_units": (i, [vp, i]),
+        "moe_gpu_read_trace": (i, [vp, vp, i, C.POINTER(i)]),
         "moe_gpu_get_option": (i, [vp, i, C.POINTER(i)]),
         "moe_gpu_profile_kernels": (i, [vp, i]),
         "moe_gpu_profile_slots": (i, []),
@@ -211,6 +213,16 @@ class MoeGpu:
         v = C.c_int()
         self._chk(self.L.moe_gpu_get_option(self.h, opt, C.byref(v)))
         return int(v.value)
+
+    def trace_units(self, on: bool = True):
+        self._chk(self.L.moe_gpu_trace_units(self.h, 1 if on else 0))
+
+    def read_trace(self) -> np.ndarray:
+        """[units, 4] uint64: start, dependencies met, end (100 MHz ticks), workgroup — of the last fused launch."""
+        cap = 1 << 16
+        buf = np.zeros((cap, 4), np.uint64); n = C.c_int()
+        self._chk(self.L.moe_gpu_read_trace(self.h, _p(buf), cap, C.byref(n)))
+        return buf[: n.value].copy()
 
     def profile_kernels(self, on: bool = True):
         self._chk(self.L.moe_gpu_profile_kernels(self.h, 1 if on else 0))

@@ -337,3 +337,44 @@ def test_fused_repeated_calls_stay_consistent(solar):
     for _ in range(20):
         again, _, _ = tier.layer(0, x)
         np.testing.assert_array_equal(again.view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize("fused", [1, 0])
+def test_solar_routed_only_ck_moe3_semantics(solar, fused):
+    """moe_placed on a tier with a shared expert: routed-only sum, accumulated into the caller's out (ck_moe3)."""
+    from moe_gpu import OPT_FUSED
+    tier, hl = solar
+    rng = np.random.default_rng(100 + fused)
+    x = random_x(1, SOLAR.H, rng)[0]
+    ids, w = [3, 64, 127, 0], np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    out0 = rng.normal(0, 1, SOLAR.H).astype(np.float32)
+    got = out0.copy()
+    say(f"solar moe_placed fused={fused}")
+    tier.set_option(OPT_FUSED, fused)
+    try:
+        tier.moe_placed(0, ids, w, x, got)
+    finally:
+        tier.set_option(OPT_FUSED, 1)
+    exp = out0.copy()
+    bases = [np.concatenate([a.ravel() for a in hl.expert(e)]) for e in ids]
+    O.ck_moe3(bases, w, x, exp, SOLAR.H, SOLAR.F)
+    assert_layer_close(got, exp)
+
+
+def test_fused_varied_calls_match_unfused(solar):
+    """Back-to-back fused calls with changing T and inputs: every call equals the one-kernel-per-phase path, so no
+    workgroup reads stale routing, act or partial outputs from an earlier call."""
+    from moe_gpu import OPT_FUSED
+    tier, hl = solar
+    rng = np.random.default_rng(110)
+    xs = [random_x(int(rng.integers(1, 9)), SOLAR.H, rng) for _ in range(12)]
+    say("solar fused varied calls")
+    tier.set_option(OPT_FUSED, 1)
+    fused = [tier.layer(0, x)[0] for x in xs]
+    tier.set_option(OPT_FUSED, 0)
+    try:
+        for x, f in zip(xs, fused):
+            u = tier.layer(0, x)[0]
+            np.testing.assert_array_equal(f.view(np.uint32), u.view(np.uint32))
+    finally:
+        tier.set_option(OPT_FUSED, 1)
