@@ -124,18 +124,25 @@ uint64_t moe_gpu_synth_key(uint64_t seed, uint64_t tensor_id);
 /* Duration in ms of the last compute call's kernels when timing is enabled (hipEvents on the context stream). */
 int moe_gpu_enable_timing(moe_gpu* ctx, int on);
 int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
-/* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent cooperative kernel that
- * walks router rows, top-k/grouping, gate|up tiles and down tiles (a work queue with on-device dependency counters); 0 runs one
- * kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in workgroups
- * per CU (0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused launch. */
+/* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent kernel that walks router
+ * rows, top-k/grouping, gate|up tile parts and down tiles (a work queue with on-device dependency counters); 0 runs
+ * one kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in
+ * workgroups per CU (default 1; 0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused
+ * launch.  MOE_GPU_OPT_KSPLIT: K parts per gate|up tile, 1, 2 or 4 (0 = automatic: about 256 KiB of weights per part); it
+ * changes the summation order, identically in both paths.  MOE_GPU_OPT_LAG: fused queue order, a routed slot's down
+ * tiles are queued after the gate|up parts of the routed slot `lag` places later (0 = automatic).  MOE_GPU_OPT_SHARED_WAITS: 1
+ * holds the shared experts' gate|up parts until the routing is known (0 = stream them while routing). */
 #define MOE_GPU_OPT_FUSED 1
 #define MOE_GPU_OPT_WG_PER_CU 2
 #define MOE_GPU_OPT_LAST_GRID 3
+#define MOE_GPU_OPT_KSPLIT 4
+#define MOE_GPU_OPT_LAG 5
+#define MOE_GPU_OPT_SHARED_WAITS 6
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
  * {start, dependencies met (0 if none), end, workgroup} in the 100 MHz s_memrealtime clock; read_trace copies the
- * last launch's records (4 uint64 per unit, unit order: router rows, route, gate|up slot-major, down slot-major). */
+ * last launch's records (4 uint64 per unit, in the fused kernel's unit order). */
 int moe_gpu_trace_units(moe_gpu* ctx, int on);
 int moe_gpu_read_trace(moe_gpu* ctx, uint64_t* buf, int max_units, int* units);
 /* Per-kernel profiling: with on != 0 every kernel launched by the compute calls is bracketed by a hipEvent pair on the

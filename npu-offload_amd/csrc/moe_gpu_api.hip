@@ -51,13 +51,14 @@ struct moe_gpu {
     std::vector<Layer> layers;
     uint16_t* d_x = nullptr;
     float* d_out = nullptr;
-    float* d_logits = nullptr;
+    float* d_logits = nullptr;      // plain router logits (route() readback)
+    uint64_t* d_logits_tag = nullptr;  // tagged router logits read by the routing units
     int32_t* d_ids = nullptr;
     float* d_gates = nullptr;
     Slots* d_slots = nullptr;
     Sync* d_sync = nullptr;
-    uint16_t* d_act = nullptr;
-    float* d_ypart = nullptr;
+    uint64_t* d_act = nullptr;      // tagged SiLU(g)*u pairs
+    uint64_t* d_ypart = nullptr;    // tagged down outputs
     uint16_t* d_stage = nullptr;  // 3*F*H bf16 staging for host loads
     int8_t* d_stage_q8 = nullptr;
     float* d_stage_sc = nullptr;
@@ -67,8 +68,14 @@ struct moe_gpu {
     uint64_t* d_trace = nullptr;  // fused-kernel unit trace (allocated when tracing is switched on)
     int trace_units = 0;
     bool fused = true;     // one persistent kernel per layer call (MOE_GPU_OPT_FUSED)
-    int wg_per_cu = 0;     // fused grid: workgroups per CU, 0 = as many as fit (MOE_GPU_OPT_WG_PER_CU)
+    int wg_per_cu = 1;     // fused grid: workgroups per CU, 0 = as many as fit (MOE_GPU_OPT_WG_PER_CU)
     int last_grid = 0;
+    int ksplit = 0;        // K parts per gate|up tile, 0 = automatic (MOE_GPU_OPT_KSPLIT)
+    int lag = 0;           // fused queue lag of down blocks, 0 = automatic (MOE_GPU_OPT_LAG)
+    int shared_waits = 0;  // MOE_GPU_OPT_SHARED_WAITS
+    uint64_t* d_gpart = nullptr;    // tagged split gate|up partial sums
+    unsigned epoch = 0;             // tag of the last call (tags are never 0)
+    size_t act_bytes = 0, ypart_bytes = 0, gpart_bytes = 0, logits_tag_bytes = 0;
     // per-kernel profiling: event pairs recorded around each launch, resolved on read
     bool profiling = false;
     std::vector<hipEvent_t> prof_pool;
@@ -256,10 +263,42 @@ int prof_resolve(moe_gpu* c) {
         if ((rc_ = prof_mark((c), (kid)))) return rc_; \
     } while (0)
 
+// Zero every tagged buffer (tag 0 is never a call's epoch).
+int clear_tags(moe_gpu* c) {  // a fill kernel, not hipMemsetAsync: safe inside a caller's graph capture
+    HIPCHK(c, moe::launch_zero(c->d_logits_tag, c->logits_tag_bytes / 8, c->stream));
+    HIPCHK(c, moe::launch_zero(c->d_act, c->act_bytes / 8, c->stream));
+    HIPCHK(c, moe::launch_zero(c->d_ypart, c->ypart_bytes / 8, c->stream));
+    HIPCHK(c, moe::launch_zero(c->d_gpart, c->gpart_bytes / 8, c->stream));
+    return MOE_GPU_OK;
+}
+
+// A fresh tag for the next call.  After 2^32 - 1 calls the tags wrap: the buffers are cleared so that no word of an
+// old call can carry the new tag.
+int next_epoch(moe_gpu* c, unsigned* ep) {
+    if (++c->epoch == 0) {
+        int rc = clear_tags(c);
+        if (rc) return rc;
+        c->epoch = 1;
+    }
+    *ep = c->epoch;
+    return MOE_GPU_OK;
+}
+
+// K parts per gate|up tile: the option, else about 256 KiB of weights per part (64 rows x H / kp), the size that
+// measured best for the fused schedule at H = 4096 (smaller parts add per-unit latency, larger ones a longer tail).
+static int kparts(const moe_gpu* c, bool int8) {
+    if (c->ksplit > 0) return c->ksplit;
+    const size_t tile = (size_t)64 * c->d.H * (int8 ? 1 : 2);
+    int kp = 1;
+    while (kp < 4 && tile / (kp * 2) >= ((size_t)256 << 10)) kp *= 2;
+    return kp;
+}
+
 // The expert pipeline of one call.  do_topk: route on the device from the layer's router (ids/gates are outputs);
 // otherwise ids/gates are the caller's routing.  Fused: one persistent kernel; unfused: one kernel per phase.
 int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, float* gates, bool do_topk, int keep,
               int n_shared, unsigned flags, float* out) {
+    int rc;
     ExpertArgs a;
     a.L = ptrs(c, layer);
     a.d = c->d;
@@ -269,24 +308,32 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
     a.x = x; a.out = out; a.ids = ids; a.gates = gates;
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
+    a.kp = kparts(c, a.int8 != 0);
+    a.gpart = c->d_gpart;
+    if ((rc = next_epoch(c, &a.epoch))) return rc;
+    a.err = &c->d_sync->err;
     if (c->fused) {
         FusedArgs f;
         f.e = a;
-        f.logits = c->d_logits;
+        f.logits = c->d_logits_tag;
         f.sync = c->d_sync;
         f.nR = do_topk ? (c->d.E + moe::kWaves - 1) / moe::kWaves : 0;
         f.do_topk = do_topk ? 1 : 0;
         f.trace = c->d_trace;
-        c->trace_units = f.nR + 1 + a.maxs * (c->d.F / 32) + a.maxs * (c->d.H / 64);
+        f.lag = c->lag > 0 ? c->lag : 8;
+        f.shared_waits = c->shared_waits;
+        c->trace_units = moe::fused_units(f.nR, a.maxs, c->d.F, c->d.H, a.kp);
         LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->stream, &c->last_grid));
         return MOE_GPU_OK;
     }
-    if (do_topk) LAUNCH(c, K_ROUTER, moe::launch_router(a.L, c->d, T, x, c->d_logits, c->stream));
+    if (do_topk)
+        LAUNCH(c, K_ROUTER, moe::launch_router(a.L, c->d, T, x, c->d_logits_tag, nullptr, a.epoch, c->stream));
     // slots 0 .. d.n_shared-1 are always the shared experts' (summed only when this call includes them)
-    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, c->d.n_shared, do_topk, c->d_logits, ids, gates,
+    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, c->d.n_shared, do_topk, c->d_logits_tag, a.epoch,
+                                             a.err, ids, gates,
                                              c->d_slots, c->stream));
-    LAUNCH(c, K_GATEUP, moe::launch_gateup(a, c->stream));
-    LAUNCH(c, K_DOWN, moe::launch_down(a, c->d_sync, c->stream));
+    LAUNCH(c, K_GATEUP, moe::launch_gateup(a, c->d_sync, c->stream));
+    LAUNCH(c, K_DOWN, moe::launch_down(a, c->stream));
     return MOE_GPU_OK;
 }
 
@@ -366,16 +413,24 @@ int moe_gpu_create(int device, int H, int F, int E, int topk, int n_shared, int 
     if ((rc = dev_alloc(c, (void**)&c->d_x, (size_t)max_tokens * H * 2, "x"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_out, (size_t)max_tokens * H * 4, "out"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_logits, (size_t)max_tokens * E * 4, "logits"))) return bail(rc);
+    c->logits_tag_bytes = (size_t)max_tokens * E * 8;
+    if ((rc = dev_alloc(c, (void**)&c->d_logits_tag, c->logits_tag_bytes, "tagged logits"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_ids, (size_t)max_tokens * topk * 4, "ids"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_gates, (size_t)max_tokens * topk * 4, "gates"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_slots, sizeof(Slots), "slots"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_sync, sizeof(Sync), "sync counters"))) return bail(rc);
-    if ((rc = dev_alloc(c, (void**)&c->d_act, (size_t)maxs * max_tokens * F * 2, "act"))) return bail(rc);
-    if ((rc = dev_alloc(c, (void**)&c->d_ypart, (size_t)max_tokens * kq * H * 4, "ypart"))) return bail(rc);
+    c->act_bytes = (size_t)maxs * max_tokens * (F / 2) * 8;
+    c->ypart_bytes = (size_t)max_tokens * kq * H * 8;
+    if ((rc = dev_alloc(c, (void**)&c->d_act, c->act_bytes, "act"))) return bail(rc);
+    if ((rc = dev_alloc(c, (void**)&c->d_ypart, c->ypart_bytes, "ypart"))) return bail(rc);
+    // split gate|up partials: at most max_tokens * (n_shared + topk) (slot, token) pairs, 4 parts per tile
+    c->gpart_bytes = (size_t)max_tokens * kq * (F / 32) * 4 * 64 * 8;
+    if ((rc = dev_alloc(c, (void**)&c->d_gpart, c->gpart_bytes, "gate|up partials"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage, (size_t)3 * F * H * 2, "staging"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage_q8, (size_t)3 * F * H, "int8 staging"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage_sc, (size_t)(2 * F + H) * 4, "scale staging"))) return bail(rc);
-    if (hipMemset(c->d_slots, 0, sizeof(Slots)) != hipSuccess || hipMemset(c->d_sync, 0, sizeof(Sync)) != hipSuccess)
+    if (hipMemset(c->d_slots, 0, sizeof(Slots)) != hipSuccess || hipMemset(c->d_sync, 0, sizeof(Sync)) != hipSuccess ||
+        clear_tags(c) != MOE_GPU_OK || hipStreamSynchronize(c->stream) != hipSuccess)
         return bail(fail(c, MOE_GPU_EHIP, "hipMemset of the workspace failed"));
     if (const char* v = getenv("MOE_GPU_FUSED")) c->fused = atoi(v) != 0;
     if (const char* v = getenv("MOE_GPU_WG_PER_CU")) c->wg_per_cu = atoi(v);
@@ -394,8 +449,8 @@ void moe_gpu_destroy(moe_gpu* c) {
         for (void* p : ps)
             if (p) (void)hipFree(p);
     }
-    void* ws[] = {c->d_x, c->d_out, c->d_logits, c->d_ids, c->d_gates, c->d_slots, c->d_sync, c->d_act, c->d_ypart,
-                  c->d_stage, c->d_stage_q8, c->d_stage_sc};
+    void* ws[] = {c->d_x, c->d_out, c->d_logits, c->d_logits_tag, c->d_ids, c->d_gates, c->d_slots, c->d_sync,
+                  c->d_act, c->d_ypart, c->d_gpart, c->d_stage, c->d_stage_q8, c->d_stage_sc};
     for (void* p : ws)
         if (p) (void)hipFree(p);
     for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
@@ -544,10 +599,12 @@ int moe_gpu_route_dev(moe_gpu* c, int layer, int T, const uint16_t* x, int keep,
     if (!x || !ids || !gates) return fail(c, MOE_GPU_EINVAL, "NULL x/ids/gates");
     keep = norm_keep(c, keep);
     const LayerPtrs L = ptrs(c, layer);
-    float* lg = logits ? logits : c->d_logits;
+    unsigned ep = 0;
+    if ((rc = next_epoch(c, &ep))) return rc;
     if ((rc = begin_timing(c))) return rc;
-    LAUNCH(c, K_ROUTER, moe::launch_router(L, c->d, T, x, lg, c->stream));
-    LAUNCH(c, K_TOPK, moe::launch_topk_group(L, c->d, T, keep, c->d.n_shared, true, lg, ids, gates, c->d_slots,
+    LAUNCH(c, K_ROUTER, moe::launch_router(L, c->d, T, x, c->d_logits_tag, logits, ep, c->stream));
+    LAUNCH(c, K_TOPK, moe::launch_topk_group(L, c->d, T, keep, c->d.n_shared, true, c->d_logits_tag, ep,
+                                             &c->d_sync->err, ids, gates, c->d_slots,
                                              c->stream));
     return end_timing(c);
 }
@@ -703,6 +760,16 @@ int moe_gpu_set_option(moe_gpu* c, int opt, int value) {
             if (value < 0) return fail(c, MOE_GPU_EINVAL, "workgroups per CU %d < 0", value);
             c->wg_per_cu = value;
             return MOE_GPU_OK;
+        case MOE_GPU_OPT_KSPLIT:
+            if (value != 0 && value != 1 && value != 2 && value != 4)
+                return fail(c, MOE_GPU_EINVAL, "K split %d not in {0, 1, 2, 4}", value);
+            c->ksplit = value;
+            return MOE_GPU_OK;
+        case MOE_GPU_OPT_LAG:
+            if (value < 0) return fail(c, MOE_GPU_EINVAL, "lag %d < 0", value);
+            c->lag = value;
+            return MOE_GPU_OK;
+        case MOE_GPU_OPT_SHARED_WAITS: c->shared_waits = value != 0; return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
 }
@@ -711,8 +778,8 @@ int moe_gpu_trace_units(moe_gpu* c, int on) {
     int rc = enter(c);
     if (rc) return rc;
     if (on && !c->d_trace) {
-        const size_t units = (size_t)(c->d.E + moe::kWaves - 1) / moe::kWaves + 1 +
-                             (size_t)(c->d.n_shared + c->d.max_t * c->d.k) * (c->d.F / 32 + c->d.H / 64);
+        const size_t units = (size_t)moe::fused_units((c->d.E + moe::kWaves - 1) / moe::kWaves,
+                                                      c->d.n_shared + c->d.max_t * c->d.k, c->d.F, c->d.H, 4);
         if ((rc = dev_alloc(c, (void**)&c->d_trace, units * 4 * sizeof(uint64_t), "unit trace"))) return rc;
         HIPCHK(c, hipMemset(c->d_trace, 0, units * 4 * sizeof(uint64_t)));
     } else if (!on && c->d_trace) {
@@ -743,6 +810,9 @@ int moe_gpu_get_option(moe_gpu* c, int opt, int* value) {
         case MOE_GPU_OPT_FUSED: *value = c->fused ? 1 : 0; return MOE_GPU_OK;
         case MOE_GPU_OPT_WG_PER_CU: *value = c->wg_per_cu; return MOE_GPU_OK;
         case MOE_GPU_OPT_LAST_GRID: *value = c->last_grid; return MOE_GPU_OK;
+        case MOE_GPU_OPT_KSPLIT: *value = c->ksplit; return MOE_GPU_OK;
+        case MOE_GPU_OPT_LAG: *value = c->lag; return MOE_GPU_OK;
+        case MOE_GPU_OPT_SHARED_WAITS: *value = c->shared_waits; return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
 }

@@ -27,6 +27,9 @@ struct Slots {
     int ntok[kMaxSlots];
     int tok[kMaxSlots][kMaxTokens];
     int rank[kMaxSlots][kMaxTokens];  // routed: rank of this expert in token tok's top-k; shared: -1
+    int pair[kMaxSlots];              // first (slot, token) pair of the slot: shared s -> s * T, routed slots follow
+    int vid[kMaxTokens * kMaxTopk];   // [t][k] expert whose down output the combine reads; -1: none (empty/dropped)
+    float vgate[kMaxTokens * kMaxTopk];  // [t][k] gate used by the combine
 };
 
 // Where a layer's weights live.  Routed expert e's bf16 gate|up table starts at gu + e * gu_stride (elements), its down
@@ -70,46 +73,53 @@ struct ExpertArgs {
     int32_t* ids;                             // [T][k]
     float* gates;                             // [T][k]
     Slots* slots;
-    uint16_t* act;                            // [maxs][max_t][F] bf16
-    float* ypart;                             // [T][n_shared + k][H] fp32
+    // cross-workgroup intermediates, tagged words (epoch << 32) | payload
+    uint64_t* act;                            // [maxs][max_t][F/2] pairs of bf16 SiLU(g)*u
+    uint64_t* ypart;                          // [T][n_shared + k][H] fp32 down outputs
+    uint64_t* gpart;                          // [pairs][F/32][kp][64] fp32 partial sums of split gate|up tiles
+    int kp;                                   // K parts of a gate|up tile (1, 2 or 4): one unit each
+    unsigned epoch;                           // this call's tag (never 0)
+    unsigned* err;                            // set when a bounded wait gave up (sticky until the host clears it)
 };
 
-// Dependency counters of the fused kernel (zero between launches; the last workgroup of a launch clears them).
-// Every counter sits in its own 128-byte line so that pollers of one counter do not contend with another's.
-constexpr int kSyncPad = 32;  // unsigneds per counter
+// Work-queue heads of the fused kernel.  A launch with epoch n hands out units from next_unit[n & 1] and clears
+// next_unit[(n + 1) & 1] for the next launch; each head sits in its own 128-byte line.
+constexpr int kSyncPad = 32;  // unsigneds per line
 struct Sync {
-    unsigned router_done;
-    unsigned pad0_[kSyncPad - 1];
-    unsigned route_ready;
-    unsigned pad1_[kSyncPad - 1];
-    unsigned exit_count;
-    unsigned pad2_[kSyncPad - 1];
     unsigned err;  // set when a bounded wait gave up (sticky until the host clears it)
-    unsigned pad3_[kSyncPad - 1];
-    unsigned next_unit;  // work-queue head of the fused kernel
-    unsigned pad4_[kSyncPad - 1];
-    unsigned gu_done[kMaxSlots * kSyncPad];
-    unsigned d_done[kMaxHTiles * kSyncPad];
+    unsigned pad0_[kSyncPad - 1];
+    unsigned next_unit[2 * kSyncPad];
 };
 
 struct FusedArgs {
     ExpertArgs e;
-    float* logits;  // [T][E]
+    uint64_t* logits;  // [T][E] tagged router logits
     Sync* sync;
     uint64_t* trace;  // optional: per unit {start, dependencies met, end, workgroup} in 100 MHz realtime ticks
     int nR;         // router units (0 when the caller gives ids)
     int do_topk;
+    int lag;        // queue order: routed slot s's down block follows routed slot (s + lag)'s gate|up block (lag >= 1)
+    int shared_waits;  // 1: shared gate|up parts start only once the routing is known
 };
+
+// Fused-kernel unit count: router units, the route publisher, then every slot's gate|up and down units.
+__host__ __device__ inline int fused_units(int nR, int maxs, int F, int H, int kp) {
+    return nR + 1 + maxs * (F / 32) * kp + maxs * (H / 64);
+}
 
 size_t lds_bytes(int T, int NT, int H, int F, int E);
 
 // ---- launch helpers (moe_kernels.hip) ---------------------------------------------------------------------------
-hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, float* logits, hipStream_t st);
+// logits: tagged [T][E] (always written); logits_out: optional plain fp32 copy
+hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, uint64_t* logits,
+                         float* logits_out, unsigned epoch, hipStream_t st);
 hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
-                             const float* logits, int32_t* ids, float* gates, Slots* slots, hipStream_t st);
-hipError_t launch_gateup(const ExpertArgs& a, hipStream_t st);
-// down projection + the gated combine (the last down unit of each 64-row tile combines it)
-hipError_t launch_down(const ExpertArgs& a, Sync* sync, hipStream_t st);
+                             const uint64_t* logits, unsigned epoch, unsigned* err, int32_t* ids, float* gates,
+                             Slots* slots, hipStream_t st);
+// gate|up parts; also clears the fused work-queue heads (the unfused path does not use them)
+hipError_t launch_gateup(const ExpertArgs& a, Sync* sync, hipStream_t st);
+// down projection + the gated combine (the down unit of the last slot combines each 64-row tile)
+hipError_t launch_down(const ExpertArgs& a, hipStream_t st);
 // wg_per_cu <= 0: as many workgroups per CU as fit (a plain launch: the work queue needs no co-residency);
 // grid_out receives the grid size
 hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out);
@@ -125,6 +135,7 @@ hipError_t launch_quantize(const uint16_t* gu, const uint16_t* dn, int H, int F,
 hipError_t launch_synth_tiled(uint64_t key_g, uint64_t key_u, uint64_t key_d, float c, int H, int F, uint16_t* gu,
                               uint16_t* dn, hipStream_t st);
 hipError_t launch_synth_fill(uint16_t* dst, uint64_t n, uint64_t key, uint64_t start, float c, hipStream_t st);
+hipError_t launch_zero(uint64_t* dst, size_t n, hipStream_t st);
 
 uint64_t synth_key(uint64_t seed, uint64_t tensor_id);
 // Returns true when the code object holds kernels for the current device.

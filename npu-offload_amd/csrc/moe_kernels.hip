@@ -9,9 +9,10 @@
 // workgroup in LDS and read as broadcasts, and the K range of a tile is split over the 4 wavefronts of a workgroup
 // and reduced through LDS in a fixed order.
 //
-// The work of one layer call is a list of units — router rows, the top-k/grouping unit, gate|up tiles, down tiles —
-// executed either by one kernel per phase (the unfused path) or by one persistent cooperative kernel that walks the
-// list with dependency counters (the fused path).  Both paths run the same unit functions, so they agree bit for bit.
+// The work of one layer call is a list of units — router rows, the top-k/grouping unit, gate|up tile parts, down
+// tiles — executed either by one kernel per phase (the unfused path) or by one persistent kernel that walks the list
+// through a work queue (the fused path).  Cross-workgroup values are epoch-tagged words that consumers poll directly.
+// Both paths run the same unit functions, so they agree bit for bit.
 #include "moe_kernels.h"
 
 #include <math.h>
@@ -24,10 +25,14 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 // would share the vector-memory counter with the in-flight weight stream.
 #define LDS_AS __attribute__((address_space(3)))
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef LDS_AS u32x4 lds_u32x4;
 typedef LDS_AS float lds_float;
 
 constexpr unsigned kSpinLimit = 1u << 20;  // bounded dependency waits (~1 s): a wait never hangs the GPU
+// Shared-memory scratch of route_local (carved from the act-row region, unused while a unit computes its routing).
+constexpr int kRouteKeys = 1024;  // sort keys of one pass (tokens x experts)
+constexpr size_t kRouteScratchBytes = (size_t)kRouteKeys * 8 + (size_t)kRouteKeys * 4;
 
 __device__ __forceinline__ float bf_lo(unsigned v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf_hi(unsigned v) { return __uint_as_float(v & 0xFFFF0000u); }
@@ -56,17 +61,46 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.f +
 
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
-// Data that crosses workgroups inside one launch (logits, the slot table, ids/gates, act, partial outputs) is written
-// and read with agent-scope relaxed atomics: on gfx950 these are plain global loads/stores carrying the sc1 bit, which
-// keeps them coherent across the XCDs' L2s without any cache writeback or invalidate.  A producer orders its data
-// before the counter it bumps by waiting for its own stores to complete (vmcnt(0)) before the workgroup barrier; a
-// consumer reads the data only after it has observed the counter.  Agent-scope fences (an L2 writeback/invalidate per
-// wavefront, microseconds each under load) are never needed on the hot path.
+// Data that crosses workgroups inside one launch is written and read with agent-scope relaxed atomics: on gfx950 these
+// are plain global loads/stores carrying the sc1 bit, coherent across the XCDs' L2s without any cache writeback or
+// invalidate.  Every such value is a 64-bit word (epoch << 32) | payload, stored with one store and read with one load
+// (single-copy atomic): the host gives each call a fresh epoch, so a consumer that reads a word carrying the call's
+// epoch holds a value of this call.  Consumers poll the data itself (bounded); producers never wait for their stores
+// to complete, and there are no dependency counters, so each dependency costs one memory round trip.
 template <typename V>
 __device__ __forceinline__ V ld_sync(const V* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 template <typename V>
 __device__ __forceinline__ void st_sync(V* p, V v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void wait_own_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0), others untouched
+
+__device__ __forceinline__ void st_tag(uint64_t* p, unsigned epoch, unsigned v) {
+    st_sync(p, ((uint64_t)epoch << 32) | v);
+}
+__device__ __forceinline__ bool tag_ok(uint64_t w, unsigned epoch) { return (unsigned)(w >> 32) == epoch; }
+
+// Words w[m] (m < M, loaded earlier from ptr(m), needed where need(m)) that do not carry the epoch yet are re-loaded
+// together, one round trip per pass, until all do.  Gives up after kSpinLimit passes, or early once another wait of
+// the launch gave up (err set), so no wait can hang the GPU; the host then reports the call as failed.
+template <int M, typename Ptr, typename Need>
+__device__ __forceinline__ void settle(uint64_t (&w)[M], Ptr ptr, Need need, unsigned epoch, unsigned* err) {
+    auto pending = [&]() {
+        bool p = false;
+#pragma unroll
+        for (int m = 0; m < M; m++) p = p || (need(m) && !tag_ok(w[m], epoch));
+        return p;
+    };
+    unsigned n = 0;
+    while (pending()) {
+        ++n;
+        if (n > kSpinLimit || ((n & 255) == 0 && ld_sync(err))) {
+            st_sync(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            if (need(m) && !tag_ok(w[m], epoch)) w[m] = ld_sync(ptr(m));
+    }
+}
 
 // wavefront index within the workgroup as a wave-uniform (scalar) value, so loop bounds derived from it stay scalar
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -130,45 +164,66 @@ __device__ __forceinline__ void dot_chunk_q8(const u32x4 w, const lds_u32x4* xs,
 
 // Stream chunks [c0, c1) of a 64-row tile (lane = row), consuming in ascending order.  Two register banks of D
 // loads alternate (load B, consume A, reload A, consume B), so D to 2D loads are always in flight and a reload only
-// ever targets a bank that has been consumed; the steady-state loop has no branches.
+// ever targets a bank that has been consumed; the steady-state loop has no branches.  begin() issues the first bank,
+// so a caller can start the stream before it waits for the activations (run() consumes them).
+#ifndef MOE_STREAM_DEPTH
+#define MOE_STREAM_DEPTH 8  // loads per register bank (1 KB each per wavefront)
+#endif
 template <int N, bool Q8>
-__device__ __forceinline__ void tile_stream(const u32x4* __restrict__ tile, int c0, int c1, const lds_u32x4* xs,
-                                            const int* xoff, float* acc) {
-    constexpr int D = N >= 8 ? 4 : 8;  // wide token counts hold N activation chunks per weight chunk in registers
-    const u32x4* p = tile + (threadIdx.x & 63);
-    u32x4 A[D], B[D];
-    auto load = [&](u32x4* bank, int c) {
+struct TileStream {
+    // wide token counts hold N activation chunks per weight chunk in registers: at most 4 loads per bank
+    static constexpr int D = N >= 8 ? (MOE_STREAM_DEPTH < 4 ? MOE_STREAM_DEPTH : 4) : MOE_STREAM_DEPTH;
+    const u32x4* p;
+    int c0, c1;
+    u32x4 A[D];
+    __device__ __forceinline__ void load(u32x4* bank, int c) {
 #pragma unroll
         for (int u = 0; u < D; u++) bank[u] = ld_stream(p + (size_t)(c + u) * 64);
-    };
-    auto consume = [&](const u32x4* bank, int c) {
+    }
+    __device__ __forceinline__ void consume(const u32x4* bank, int c, const lds_u32x4* xs, const int* xoff, float* acc) {
 #pragma unroll
         for (int u = 0; u < D; u++) {
             if (Q8) dot_chunk_q8<N>(bank[u], xs, xoff, c + u, acc);
             else dot_chunk_bf16<N>(bank[u], xs, xoff, c + u, acc);
         }
-    };
-    const int nb = (c1 - c0) / D;
-    int b = 0;
-    if (nb > 0) load(A, c0);
-    for (; b + 2 < nb; b += 2) {
-        load(B, c0 + (b + 1) * D);
-        consume(A, c0 + b * D);
-        load(A, c0 + (b + 2) * D);
-        consume(B, c0 + (b + 1) * D);
     }
-    if (nb - b == 2) {
-        load(B, c0 + (b + 1) * D);
-        consume(A, c0 + b * D);
-        consume(B, c0 + (b + 1) * D);
-    } else if (nb - b == 1) {
-        consume(A, c0 + b * D);
+    __device__ __forceinline__ void begin(const u32x4* __restrict__ tile, int c0_, int c1_) {
+        p = tile + (threadIdx.x & 63);
+        c0 = c0_;
+        c1 = c1_;
+        if ((c1 - c0) / D > 0) load(A, c0);
     }
-    for (int c = c0 + nb * D; c < c1; c++) {  // fewer than D leftover chunks
-        const u32x4 w = ld_stream(p + (size_t)c * 64);
-        if (Q8) dot_chunk_q8<N>(w, xs, xoff, c, acc);
-        else dot_chunk_bf16<N>(w, xs, xoff, c, acc);
+    __device__ __forceinline__ void run(const lds_u32x4* xs, const int* xoff, float* acc) {
+        u32x4 B[D];
+        const int nb = (c1 - c0) / D;
+        int b = 0;
+        for (; b + 2 < nb; b += 2) {
+            load(B, c0 + (b + 1) * D);
+            consume(A, c0 + b * D, xs, xoff, acc);
+            load(A, c0 + (b + 2) * D);
+            consume(B, c0 + (b + 1) * D, xs, xoff, acc);
+        }
+        if (nb - b == 2) {
+            load(B, c0 + (b + 1) * D);
+            consume(A, c0 + b * D, xs, xoff, acc);
+            consume(B, c0 + (b + 1) * D, xs, xoff, acc);
+        } else if (nb - b == 1) {
+            consume(A, c0 + b * D, xs, xoff, acc);
+        }
+        for (int c = c0 + nb * D; c < c1; c++) {  // fewer than D leftover chunks
+            const u32x4 w = ld_stream(p + (size_t)c * 64);
+            if (Q8) dot_chunk_q8<N>(w, xs, xoff, c, acc);
+            else dot_chunk_bf16<N>(w, xs, xoff, c, acc);
+        }
     }
+};
+
+template <int N, bool Q8>
+__device__ __forceinline__ void tile_stream(const u32x4* __restrict__ tile, int c0, int c1, const lds_u32x4* xs,
+                                            const int* xoff, float* acc) {
+    TileStream<N, Q8> ts;
+    ts.begin(tile, c0, c1);
+    ts.run(xs, xoff, acc);
 }
 
 // Sum the 4 wavefronts' partials in wave order; result for (token j, row lane) in red[j * 64 + lane].
@@ -194,17 +249,18 @@ __device__ __forceinline__ void reduce_waves(lds_float* red, const float* acc, i
 //   xs    [T][H/8] u32x4      all tokens' activations, staged once per workgroup
 //   as    [NT][F/8] u32x4     one slot's act rows (down units)
 //   red   [4][NT][64] float   cross-wave reduction
-// (the route unit's scratch is static __shared__ memory inside route_unit)
+// (the routing table is static __shared__ memory: RouteTab)
 struct Lds {
     lds_u32x4* xs;
     lds_u32x4* as;
     lds_float* red;
 };
 
-// `as` doubles as the route unit's score table: NT tokens x E (rounded up to 4) biased scores + NT x topk ranks.
+// `as` also serves as route_local's scratch
 __host__ __device__ inline size_t as_bytes(int NT, int F, int E) {
-    const size_t act = (size_t)NT * (F / 8) * 16, route = (size_t)NT * (((E + 3) & ~3) + kMaxTopk) * 4;
-    return ((act > route ? act : route) + 15) & ~(size_t)15;
+    (void)E;
+    const size_t act = (size_t)NT * (F / 8) * 16;
+    return act > kRouteScratchBytes ? act : kRouteScratchBytes;
 }
 
 size_t lds_bytes(int T, int NT, int H, int F, int E) {
@@ -233,22 +289,29 @@ __device__ inline void stage_x(const Lds& s, const uint16_t* __restrict__ x, int
 // Unit: router rows.  Wave w computes logits[t, e] for e = e0 + w and all T tokens.  Reduction order (mirrored bit
 // for bit by the host oracle): lane l owns chunks c = l + 64 j; per token a fused multiply-add chain over j
 // ascending and elements 0..7 ascending; then a 64-lane xor butterfly (32, 16, 8, 4, 2, 1).
+// x_stage: when not null the activations are staged here, after the first block of weight loads is in flight.
 template <int NT>
 __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
-                            float* __restrict__ logits) {
+                                            uint64_t* __restrict__ logits, float* __restrict__ logits_out,
+                                            unsigned epoch, const uint16_t* __restrict__ x_stage) {
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int e = e0 + wave;
-    if (e >= E) return;
-    const u32x4* row = reinterpret_cast<const u32x4*>(wr + (size_t)e * H);
+    const u32x4* row = reinterpret_cast<const u32x4*>(wr + (size_t)min(e, E - 1) * H);
     const int nc = H / 8, nj = H / 512;
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.f;
-    for (int j0 = 0; j0 < nj; j0 += 8) {
-        u32x4 w[8];
+    u32x4 w[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j0 + j < nj) w[j] = row[lane + 64 * (j0 + j)];
+    for (int j = 0; j < 8; j++)
+        if (j < nj) w[j] = row[lane + 64 * j];
+    if (x_stage) stage_x(s, x_stage, T, H);
+    for (int j0 = 0; j0 < nj; j0 += 8) {
+        if (j0 > 0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (j0 + j < nj) w[j] = row[lane + 64 * (j0 + j)];
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (j0 + j < nj) {
@@ -267,203 +330,304 @@ __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __rest
             }
         }
     }
+    if (e >= E) return;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         if (t < T) {
             float v = acc[t];
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            if (lane == 0) st_sync(&logits[(size_t)t * E + e], v);
+            if (lane == 0) {
+                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(v));
+                if (logits_out) logits_out[(size_t)t * E + e] = v;
+            }
         }
     }
 }
 
 // --------------------------------------------------------------------------------------------------------------------
-// Unit: softmax top-k (one wavefront per token, tokens strided over the 4 waves) and expert grouping (workgroup).
-// Selection compares biased logits, ties to the lower expert index; gates = softmax restricted to the kept ranks.
-// Grouping: routed slots in first-seen order scanning tokens then ranks; shared slots first.
-// Maximum over the 64 lanes of a wavefront: DPP exchanges within rows of 16 lanes, then the four row results.
-__device__ __forceinline__ float dpp_max_step(float v, int ctrl_id) {
-    int o;
-    switch (ctrl_id) {  // dpp_ctrl must be a compile-time constant
-        case 0: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
-        case 1: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
-        case 2: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
-        default: o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
-    }
-    return fmaxf(v, __int_as_float(o));
+// Routing.
+// Per-workgroup routing table in shared memory.  Every workgroup of the fused kernel that needs the routing computes
+// it itself from the logits (the computation is deterministic, so all copies agree bit for bit) instead of waiting
+// for one workgroup to publish it: this removes a publish / poll / reload hop from the critical path.
+struct RouteTab {
+    int nslot;
+    int err;                                          // 1: an id outside [-1, E); 2: an expert repeated in a token
+    int id[kMaxTokens * kMaxTopk];                    // [t][k] expert of rank r; -1: empty rank or dropped id
+    float gate[kMaxTokens * kMaxTopk];                // [t][k] gate of rank r (0 for ranks >= keep)
+    short slot_e[kMaxSlots];                          // expert of a slot (shared slot s: -1 - s)
+    unsigned char slot_n[kMaxSlots];                  // tokens of a slot
+    unsigned char slot_p[kMaxSlots][kMaxTokens];      // routed slot: entry p = t * keep + r; shared slot: token
+    short slot_pair[kMaxSlots];                       // first (slot, token) pair: shared s -> s * T, then routed
+};
+typedef LDS_AS RouteTab lds_RouteTab;
+
+// Total order of the selection as one unsigned 64-bit key: biased score (NaN ranks as -inf) through the
+// order-preserving float -> uint map in the high word, the complemented expert index in the low word, so that a
+// larger key means (higher score, or equal score and lower index).
+__device__ __forceinline__ uint64_t route_key(float v, int e) {
+    const unsigned u = __float_as_uint(v);
+    const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (unsigned)~e;
 }
-__device__ __forceinline__ float wave_max(float v) {
-    v = dpp_max_step(v, 0);
-    v = dpp_max_step(v, 1);
-    v = dpp_max_step(v, 2);
-    v = dpp_max_step(v, 3);  // every lane of a 16-lane row now holds the row maximum
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+__device__ __forceinline__ float route_key_score(uint64_t key) {
+    const unsigned o = (unsigned)(key >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-__device__ __forceinline__ void route_unit(const Lds& s, const float* __restrict__ logits, const float* __restrict__ bias,
-                                           int T, int E, int k, int keep, int n_shared, int do_topk,
-                                           int32_t* __restrict__ ids, float* __restrict__ gates,
-                                           Slots* __restrict__ slots) {
-    __shared__ int ent_e[kMaxTokens * kMaxTopk];       // expert of entry (t, r), r < keep; -1 = empty rank
-    __shared__ int first_pos[kMaxExperts];
-    __shared__ int slot_of[kMaxExperts];
-    __shared__ int ent_flag[kMaxTokens * kMaxTopk];
-    const int tid = threadIdx.x;
-    const int n = T * keep;
-    if (tid == 0) st_sync(&slots->err, 0);
-    __syncthreads();
+// Softmax top-k and expert grouping into rt.  Selection: the k largest keys (score descending, index ascending);
+// each thread counts, for one (token, expert) and a slice of the experts, how many keys beat it (its rank), reading
+// the keys as shared-memory broadcasts, so the whole workgroup works on it.  Gates = softmax restricted to the kept
+// ranks: exp(s_r - s_0) / sum_{q < keep} exp(s_q - s_0), summed in rank order.  Grouping: routed slots in first-seen
+// order scanning tokens then ranks (solar_hybrid/runtime.py:344-347), after the n_shared shared slots.  do_topk == 0:
+// the caller's ids / gates are taken as given (ids outside [-1, E) dropped).  scr: kRouteScratchBytes of LDS.
+__device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned char* scr,
+                                            const uint64_t* __restrict__ logits, unsigned epoch, unsigned* err,
+                                            const float* __restrict__ bias, const int32_t* ids_in,
+                                            const float* gates_in, int T, int E, int k, int keep, int n_shared,
+                                            int do_topk) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    LDS_AS uint64_t* keys = (LDS_AS uint64_t*)scr;
+    LDS_AS int* cnt = (LDS_AS int*)(scr + (size_t)kRouteKeys * 8);
+    int bad = 0;
     if (do_topk) {
-        // One wavefront per token (tokens strided over the workgroup's wavefronts).  Lane l holds the biased scores
-        // of experts l + 64 i.  Each of the k rounds takes the maximum remaining score with a DPP reduction (no
-        // shared-memory round trips) and the lowest expert index holding it with ballots, i.e. the order is
-        // (score descending, index ascending); NaN scores rank last.
-        const int wave = wave_id(), lane = tid & 63;
-        const int nI = (E + 63) / 64;
-        for (int t0 = 0; t0 < T; t0 += kWaves) {
-            const int t = t0 + wave;
-            if (t < T) {
-                float sc[kMaxExperts / 64];
+        const int tc = min(T, max(1, kRouteKeys / E));  // tokens per pass
+        for (int t0 = 0; t0 < T; t0 += tc) {
+            const int nt = min(tc, T - t0), items = nt * E;
+            // 1. keys: every tagged logit load of the pass issued before any use (4 per thread at most)
+            constexpr int M = kRouteKeys / kThreads;
+            uint64_t w[M];
+            float b[M];
+            auto lptr = [&](int m) {
+                const int i = min(tid + m * nthr, items - 1);
+                return logits + (size_t)(t0 + i / E) * E + i % E;
+            };
+            auto lneed = [&](int m) { return tid + m * nthr < items; };
 #pragma unroll
-                for (int i = 0; i < kMaxExperts / 64; i++)  // every load issued before any use: one round trip
-                    sc[i] = ld_sync(&logits[(size_t)t * E + min(lane + 64 * i, E - 1)]);
+            for (int m = 0; m < M; m++) {
+                if (lneed(m)) {
+                    w[m] = ld_sync(lptr(m));
+                    b[m] = bias ? bias[(tid + m * nthr) % E] : 0.f;
+                }
+            }
+            settle(w, lptr, lneed, epoch, err);
 #pragma unroll
-                for (int i = 0; i < kMaxExperts / 64; i++) {
-                    const int e = lane + 64 * i;
-                    float v = sc[i] + (bias ? bias[min(e, E - 1)] : 0.f);
+            for (int m = 0; m < M; m++) {
+                if (lneed(m)) {
+                    const int i = tid + m * nthr;
+                    float v = __uint_as_float((unsigned)w[m]) + b[m];
                     if (!(v == v)) v = -INFINITY;
-                    sc[i] = e < E ? v : -INFINITY;
+                    if (v == 0.f) v = 0.f;  // -0 and +0 compare equal: one key
+                    keys[i] = route_key(v, i % E);
                 }
-                unsigned live = 0;  // bit i: element i of this lane is a real, not yet selected expert
+            }
+            __syncthreads();
+            // 2. ranks: work item (part p, item i) counts the keys of experts [p E / parts, (p + 1) E / parts) above
+            //    key i; parts spread a small pass over the whole workgroup
+            int parts = 1;  // a power of two dividing E
+            while (parts < 8 && items * parts * 2 <= nthr && E % (parts * 2) == 0) parts *= 2;
+            const int span = E / parts;  // keys compared per work item: the same count in every lane
+            for (int wi = tid; wi < items * parts; wi += nthr) {
+                const int p = wi / items, i = wi - p * items;
+                const int tl = i / E;
+                const uint64_t ki = keys[i];
+                const LDS_AS uint64_t* kr = keys + tl * E + p * span;
+                int c = 0, j = 0;
+                for (; j + 8 <= span; j += 8) {  // 8 shared-memory reads in flight, then 8 compares
+                    uint64_t kv[8];
 #pragma unroll
-                for (int i = 0; i < kMaxExperts / 64; i++)
-                    if (lane + 64 * i < E) live |= 1u << i;
-                float my_sc = 0.f;
-                int my_id = 0;
-                for (int r = 0; r < k; r++) {
-                    float lm = -INFINITY;
+                    for (int u = 0; u < 8; u++) kv[u] = kr[j + u];
 #pragma unroll
-                    for (int i = 0; i < kMaxExperts / 64; i++)
-                        if ((live >> i) & 1u) lm = fmaxf(lm, sc[i]);
-                    const float m = wave_max(lm);
-                    int id = -1;
-                    for (int i = 0; i < nI && id < 0; i++) {
-                        const unsigned long long hit = __ballot(((live >> i) & 1u) && sc[i] == m);
-                        if (hit) id = 64 * i + (__ffsll(hit) - 1);
-                    }
-                    if (id < 0) id = 0;  // unreachable: k <= E and every live score is comparable
-                    if ((id & 63) == lane) live &= ~(1u << (id >> 6));
-                    if (lane == r) { my_sc = m; my_id = id; }
+                    for (int u = 0; u < 8; u++) c += kv[u] > ki;
                 }
-                // gates: softmax restricted to the kept ranks; lane r holds rank r, rank 0 the maximum
-                const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), 0));
-                const float ex = expf(my_sc - top);
+                for (; j < span; j++) c += kr[j] > ki;
+                cnt[wi] = c;
+            }
+            __syncthreads();
+            // 3. the k best of each token, in rank order (gate slot holds the score until step 4)
+            for (int i = tid; i < items; i += nthr) {
+                int r = 0;
+                for (int p = 0; p < parts; p++) r += cnt[p * items + i];
+                if (r < k) {
+                    const int t = t0 + i / E;
+                    rt->id[t * k + r] = i % E;
+                    rt->gate[t * k + r] = route_key_score(keys[i]);
+                }
+            }
+            __syncthreads();
+            // 4. gates, one wavefront per token, lane r holding rank r
+            const int wave = wave_id(), lane = tid & 63;
+            for (int tl = wave; tl < nt; tl += nthr / 64) {
+                const int t = t0 + tl;
+                const float sc = lane < k ? rt->gate[t * k + lane] : 0.f;
+                const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), 0));
+                const float ex = expf(sc - top);
                 float tot = 0.f;
                 for (int q = 0; q < keep; q++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), q));
-                if (lane < k) {
-                    st_sync(&ids[t * k + lane], (int32_t)my_id);
-                    st_sync(&gates[t * k + lane], lane < keep ? ex / tot : 0.f);
-                    if (lane < keep) ent_e[t * keep + lane] = my_id;
+                if (lane < k) rt->gate[t * k + lane] = lane < keep ? ex / tot : 0.f;
+                if (T == 1) {  // one token's k distinct experts: slot n_shared + r holds rank r (closed-form grouping)
+                    if (lane < keep) {
+                        const int sl = n_shared + lane;
+                        rt->slot_e[sl] = (short)rt->id[lane];
+                        rt->slot_n[sl] = 1;
+                        rt->slot_p[sl][0] = (unsigned char)lane;
+                        rt->slot_pair[sl] = (short)sl;
+                    }
+                    if (lane < n_shared) {
+                        rt->slot_e[lane] = (short)(-1 - lane);
+                        rt->slot_n[lane] = 1;
+                        rt->slot_p[lane][0] = 0;
+                        rt->slot_pair[lane] = (short)lane;
+                    }
+                    if (lane == 0) {
+                        rt->nslot = n_shared + keep;
+                        rt->err = 0;
+                    }
                 }
             }
+            __syncthreads();  // keys / cnt are reused by the next pass
         }
     } else {
-        for (int p = tid; p < n; p += blockDim.x) {
-            int e = ld_sync(&ids[(p / keep) * k + p % keep]);
+        for (int p = tid; p < T * k; p += nthr) {  // the caller's routing, written before this launch
+            int e = ids_in[p];
             if (e < -1 || e >= E) {  // out of range: flag and drop the entry
-                st_sync(&slots->err, 1);
+                bad = 1;
                 e = -1;
             }
-            ent_e[p] = e;
+            rt->id[p] = e;
+            rt->gate[p] = gates_in[p];
         }
+    }
+    if (do_topk && T == 1) {  // grouped above
+        __syncthreads();
+        return;
+    }
+    bad = __syncthreads_or(bad);
+    // Grouping: thread p owns entry p = t * keep + r (n = T * keep <= 128); entries are compared through shared-memory
+    // broadcasts.  A slot's number counts the first occurrences before its own first occurrence.
+    const int n = T * keep;
+    LDS_AS int* ent = (LDS_AS int*)scr;  // entry -> expert, padded with -2 to a multiple of 4
+    LDS_AS int* fst = ent + 128;         // 1 where an entry is its expert's first occurrence
+    const int n4 = (n + 3) & ~3;
+    int my_e = -1, first = 0, pos = 0, c = 0;
+    if (tid < n4) {
+        my_e = tid < n ? rt->id[(tid / keep) * k + tid % keep] : -2;
+        ent[tid] = my_e;
     }
     __syncthreads();
-    // 4. grouping: routed slots in first-seen order scanning tokens then ranks (runtime.py:344-347), after the
-    //    n_shared shared slots.  Up to 64 entries (every decode batch of T * keep <= 64) are grouped in wave 0's
-    //    registers: lane i holds entry i, readlane/ballot replace shared-memory round trips.
-    if (n <= 64) {
-        if (tid < 64) {
-            const int lane = tid;
-            const int my_e = lane < n ? ent_e[lane] : -1;
-            int cnt = 0, pos = 0, firstj = 64;
-            for (int j = 0; j < n; j++) {
-                const int ej = __builtin_amdgcn_readlane(my_e, j);
-                const bool m = my_e >= 0 && ej == my_e;
-                cnt += m;
-                pos += m && j < lane;
-                if (m && j < firstj) firstj = j;
+    if (tid < n && my_e >= 0) {
+        first = tid;
+        for (int j = 0; j < n4; j += 4) {
+            const i32x4 q = *(const LDS_AS i32x4*)(ent + j);
+            const int v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const bool hit = v[u] == my_e;
+                c += hit;
+                pos += hit && j + u < tid;
+                if (hit && j + u < first) first = j + u;
             }
-            const bool flag = my_e >= 0 && firstj == lane;
-            const unsigned long long mask = __ballot(flag);
-            const int slot = n_shared + (int)__popcll(mask & ((1ull << firstj) - 1ull));  // slot of my first occurrence
-            if (flag) {
-                st_sync(&slots->expert[slot], my_e);
-                st_sync(&slots->ntok[slot], cnt < T ? cnt : T);
-            }
-            if (my_e >= 0) {
-                if (pos < T) {
-                    st_sync(&slots->tok[slot][pos], lane / keep);
-                    st_sync(&slots->rank[slot][pos], lane % keep);
-                } else {
-                    st_sync(&slots->err, 2);  // an expert repeated within one token's ids
-                }
-            }
-            if (lane == 0) st_sync(&slots->nslot, n_shared + (int)__popcll(mask));
-        }
-    } else {
-        for (int e = tid; e < E; e += blockDim.x) first_pos[e] = 0x7FFFFFFF;
-        __syncthreads();
-        const int my_e = tid < n ? ent_e[tid] : -1;
-        if (my_e >= 0) atomicMin(&first_pos[my_e], tid);
-        __syncthreads();
-        if (tid < n) ent_flag[tid] = my_e >= 0 && first_pos[my_e] == tid;
-        __syncthreads();
-        if (tid < n && ent_flag[tid]) {
-            int before = 0;
-            for (int j = 0; j < tid; j++) before += ent_flag[j];
-            const int sl = n_shared + before;
-            slot_of[my_e] = sl;
-            int cnt = 0;
-            for (int j = 0; j < n; j++) cnt += ent_e[j] == my_e;
-            st_sync(&slots->expert[sl], my_e);
-            st_sync(&slots->ntok[sl], cnt < T ? cnt : T);
-        }
-        __syncthreads();
-        if (my_e >= 0) {
-            const int sl = slot_of[my_e];
-            int pos = 0;
-            for (int j = 0; j < tid; j++) pos += ent_e[j] == my_e;
-            if (pos < T) {
-                st_sync(&slots->tok[sl][pos], tid / keep);
-                st_sync(&slots->rank[sl][pos], tid % keep);
-            } else {
-                st_sync(&slots->err, 2);
-            }
-        }
-        if (tid == 0) {
-            int nf = 0;
-            for (int j = 0; j < n; j++) nf += ent_flag[j];
-            st_sync(&slots->nslot, n_shared + nf);
         }
     }
+    if (tid < n4) fst[tid] = tid < n && my_e >= 0 && first == tid;
+    __syncthreads();
+    int rep = 0;
+    int before = 0;  // first occurrences before mine: a uniform loop over all entries
+    for (int j = 0; j < n4; j += 4) {
+        const i32x4 q = *(const LDS_AS i32x4*)(fst + j);
+        before += (j < first ? q.x : 0) + (j + 1 < first ? q.y : 0) + (j + 2 < first ? q.z : 0) +
+                  (j + 3 < first ? q.w : 0);
+    }
+    if (tid < n && my_e >= 0) {
+        const int slot = n_shared + before;
+        if (first == tid) {
+            rt->slot_e[slot] = (short)my_e;
+            rt->slot_n[slot] = (unsigned char)(c < T ? c : T);
+        }
+        if (pos < T) {
+            rt->slot_p[slot][pos] = (unsigned char)tid;
+        } else {  // an expert repeated within one token's ids: the extra entry is dropped
+            rt->id[(tid / keep) * k + tid % keep] = -1;
+            rep = 1;
+        }
+    }
+    const int nfirst = __syncthreads_count(tid < n && my_e >= 0 && first == tid);
+    rep = __syncthreads_or(rep);
+    if (tid == 0) {
+        rt->nslot = n_shared + nfirst;
+        rt->err = rep ? 2 : bad;
+    }
     if (tid < n_shared) {
-        st_sync(&slots->expert[tid], -1 - tid);
-        st_sync(&slots->ntok[tid], T);
-        for (int j = 0; j < T; j++) { st_sync(&slots->tok[tid][j], j); st_sync(&slots->rank[tid][j], -1); }
+        rt->slot_e[tid] = (short)(-1 - tid);
+        rt->slot_n[tid] = (unsigned char)T;
+        rt->slot_pair[tid] = (short)(tid * T);
+        for (int j = 0; j < T; j++) rt->slot_p[tid][j] = (unsigned char)j;
+    }
+    __syncthreads();
+    // pair offsets of the routed slots: exclusive prefix sum of their token counts (lane i: slots i and 64 + i)
+    if (tid < 64) {
+        const int lane = tid;
+        const int nr = rt->nslot - n_shared;
+        const int c0 = lane < nr ? rt->slot_n[n_shared + lane] : 0, c1 = 64 + lane < nr ? rt->slot_n[n_shared + 64 + lane] : 0;
+        int i0 = c0, i1 = c1;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int u0 = __shfl_up(i0, d, 64), u1 = __shfl_up(i1, d, 64);
+            if (lane >= d) {
+                i0 += u0;
+                i1 += u1;
+            }
+        }
+        const int tot0 = __shfl(i0, 63, 64);
+        if (lane < nr) rt->slot_pair[n_shared + lane] = (short)(n_shared * T + i0 - c0);
+        if (64 + lane < nr) rt->slot_pair[n_shared + 64 + lane] = (short)(n_shared * T + tot0 + i1 - c1);
     }
     __syncthreads();
 }
 
+// Write the routing outputs (ids / gates when computed here) and the global slot table used by the unfused kernels.
+__device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int k, int keep, int n_shared, int do_topk,
+                                              int32_t* __restrict__ ids, float* __restrict__ gates,
+                                              Slots* __restrict__ slots) {
+    const int tid = threadIdx.x;
+    for (int p = tid; p < T * k; p += blockDim.x) {
+        if (do_topk) {
+            st_sync(&ids[p], (int32_t)rt->id[p]);
+            st_sync(&gates[p], rt->gate[p]);
+        }
+        st_sync(&slots->vid[p], (int)rt->id[p]);
+        st_sync(&slots->vgate[p], rt->gate[p]);
+    }
+    const int ns = rt->nslot;
+    for (int i = tid; i < ns * kMaxTokens; i += blockDim.x) {
+        const int s = i / kMaxTokens, j = i % kMaxTokens;
+        if (j == 0) {
+            st_sync(&slots->expert[s], (int)rt->slot_e[s]);
+            st_sync(&slots->ntok[s], (int)rt->slot_n[s]);
+            st_sync(&slots->pair[s], (int)rt->slot_pair[s]);
+        }
+        if (j < rt->slot_n[s]) {
+            const int p = rt->slot_p[s][j];
+            st_sync(&slots->tok[s][j], s < n_shared ? p : p / keep);
+            st_sync(&slots->rank[s][j], s < n_shared ? -1 : p % keep);
+        }
+    }
+    if (tid == 0) {
+        st_sync(&slots->nslot, ns);
+        st_sync(&slots->err, rt->err);
+    }
+}
+
 // --------------------------------------------------------------------------------------------------------------------
-// Unit: gate|up tile.  Slot s, 32 f values = one 64-row tile (32 gate rows + their 32 up rows) over K = H, the 4
-// wavefronts splitting K; act[s][j][f] = bf16(silu(g) * u) for the slot's tokens.
+// Unit: gate|up tile part.  Slot s, 32 f values = one 64-row tile (32 gate rows + their 32 up rows), K part kpi of
+// a.kp (chunks [kpi, kpi + 1) * H/8/kp), the 4 wavefronts splitting the part; act[s][j][f] = bf16(silu(g) * u) for
+// the slot's tokens.  Sums: wavefronts in order within a part, then parts in order.  Parts below kp - 1 publish their
+// partial sums to gpart; part kp - 1 (the tile's last unit in queue order) reads them back, finishes the tile and
+// publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
 template <int N>
-__device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
-    const int H = a.d.H, F = a.d.F;
+__device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
+                                            const int* tok, int pair0) {
+    const int H = a.d.H, F = a.d.F, kp = a.kp, ntile = F / 32;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = H / 8;
     int xoff[N];
@@ -477,39 +641,63 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
         const uint16_t* base =
             e >= 0 ? a.L.gu + (size_t)e * a.d.gu_stride() : a.L.sgu + (size_t)(-1 - e) * a.d.gu_stride();
         const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)tile * nc * 64;
-        const int cpw = nc / kWaves;
-        tile_stream<N, false>(t, wave * cpw, (wave + 1) * cpw, s.xs, xoff, acc);
+        const int cpw = nc / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+        tile_stream<N, false>(t, c0, c0 + cpw, s.xs, xoff, acc);
     } else {
         const int ncq = H / 16;
         const u32x4* t = reinterpret_cast<const u32x4*>(a.L.gu_q8 + (size_t)e * a.d.gu_stride()) + (size_t)tile * ncq * 64;
-        const int cpw = ncq / kWaves;
-        tile_stream<N, true>(t, wave * cpw, (wave + 1) * cpw, s.xs, xoff, acc);
+        const int cpw = ncq / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+        tile_stream<N, true>(t, c0, c0 + cpw, s.xs, xoff, acc);
     }
     reduce_waves<N>(s.red, acc, N);
     if (wave == 0) {
-        const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + tile * 64 + lane] : 1.f;
+        uint64_t* gp0 = a.gpart + (((size_t)pair0 * ntile + tile) * kp) * 64 + lane;  // + (j * ntile * kp + q) * 64
+        if (kpi < kp - 1) {
 #pragma unroll
-        for (int j = 0; j < N; j++) {
-            float v = s.red[j * 64 + lane];
-            if (q8) v = v * scale;
-            const float up = __shfl_down(v, 8, 64);  // gate row lane (bit 3 clear) meets its up row (lane + 8)
-            const unsigned h = f2bf_dev(silu_mul(v, up));
-            const unsigned h_next = __shfl_down(h, 1, 64);  // f + 1 lives in the next lane
-            if (j < ntok && !gu_row_up(lane) && !(lane & 1))
-                st_sync(reinterpret_cast<unsigned*>(a.act + ((size_t)sl * a.d.max_t + j) * F + gu_row_f(tile, lane)),
-                        h | (h_next << 16));
+            for (int j = 0; j < N; j++)
+                if (j < ntok) st_tag(gp0 + ((size_t)j * ntile * kp + kpi) * 64, a.epoch, __float_as_uint(s.red[j * 64 + lane]));
+        } else {
+            const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + tile * 64 + lane] : 1.f;
+            uint64_t w[N][3];  // the other parts' partials: all loads issued before any use
+            auto gptr = [&](int j, int q) { return gp0 + ((size_t)(j < ntok ? j : 0) * ntile * kp + q) * 64; };
+#pragma unroll
+            for (int j = 0; j < N; j++)
+#pragma unroll
+                for (int q = 0; q < 3; q++)
+                    if (q < kp - 1) w[j][q] = ld_sync(gptr(j, q));
+#pragma unroll
+            for (int j = 0; j < N; j++) {
+                settle(w[j], [&](int q) { return gptr(j, q); }, [&](int q) { return q < kp - 1; }, a.epoch, a.err);
+                float v = 0.f;
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    if (q < kp - 1) {
+                        const float pv = __uint_as_float((unsigned)w[j][q]);
+                        v = q == 0 ? pv : v + pv;
+                    }
+                }
+                v = kp > 1 ? v + s.red[j * 64 + lane] : s.red[j * 64 + lane];
+                if (q8) v = v * scale;
+                const float up = __shfl_down(v, 8, 64);  // gate row lane (bit 3 clear) meets its up row (lane + 8)
+                const unsigned h = f2bf_dev(silu_mul(v, up));
+                const unsigned h_next = __shfl_down(h, 1, 64);  // f + 1 lives in the next lane
+                if (j < ntok && !gu_row_up(lane) && !(lane & 1))
+                    st_tag(a.act + ((size_t)sl * a.d.max_t + j) * (F / 2) + gu_row_f(tile, lane) / 2, a.epoch,
+                           h | (h_next << 16));
+            }
         }
     }
     __syncthreads();  // s.red is reused by the next unit
 }
 
 template <int NT>
-__device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int e, int ntok, const int* tok) {
-    if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, e, ntok, tok);
-    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, e, ntok, tok);
-    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, e, ntok, tok);
-    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8)>(s, a, sl, tile, e, ntok, tok);
-    else gateup_core<NT>(s, a, sl, tile, e, ntok, tok);
+__device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
+                                            const int* tok, int pair0) {
+    if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
+    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
+    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
+    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
+    else gateup_core<NT>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
 }
 
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
@@ -520,9 +708,38 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = F / 8;
-    const unsigned* src = reinterpret_cast<const unsigned*>(a.act + (size_t)sl * a.d.max_t * F);
+    // the weight stream starts first: its first bank is in flight while the act rows are polled
+    const bool q8 = a.int8 && e >= 0;
+    TileStream<N, false> tb;
+    TileStream<N, true> tq;
+    if (!q8) {
+        const uint16_t* base =
+            e >= 0 ? a.L.dn + (size_t)e * a.d.dn_stride() : a.L.sdn + (size_t)(-1 - e) * a.d.dn_stride();
+        const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)ht * nc * 64;
+        const int cpw = nc / kWaves;
+        tb.begin(t, wave * cpw, (wave + 1) * cpw);
+    } else {
+        const int ncq = F / 16;
+        const u32x4* t = reinterpret_cast<const u32x4*>(a.L.dn_q8 + (size_t)e * a.d.dn_stride()) + (size_t)ht * ncq * 64;
+        const int cpw = ncq / kWaves;
+        tq.begin(t, wave * cpw, (wave + 1) * cpw);
+    }
+    // the slot's act rows, published by the gate|up tiles' last parts: 8 loads per thread in flight, then polled
+    const uint64_t* src = a.act + (size_t)sl * a.d.max_t * (F / 2);
     LDS_AS unsigned* dst = (LDS_AS unsigned*)s.as;
-    for (int i = threadIdx.x; i < ntok * (F / 2); i += blockDim.x) dst[i] = ld_sync(src + i);
+    const int na = ntok * (F / 2);
+    for (int i0 = 0; i0 < na; i0 += 8 * (int)blockDim.x) {
+        uint64_t w[8];
+        auto aptr = [&](int m) { return src + i0 + m * (int)blockDim.x + (int)threadIdx.x; };
+        auto aneed = [&](int m) { return i0 + m * (int)blockDim.x + (int)threadIdx.x < na; };
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (aneed(m)) w[m] = ld_sync(aptr(m));
+        settle(w, aptr, aneed, a.epoch, a.err);
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (aneed(m)) dst[i0 + m * (int)blockDim.x + (int)threadIdx.x] = (unsigned)w[m];
+    }
     __syncthreads();
     int xoff[N];
 #pragma unroll
@@ -530,19 +747,8 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     float acc[N];
 #pragma unroll
     for (int j = 0; j < N; j++) acc[j] = 0.f;
-    const bool q8 = a.int8 && e >= 0;
-    if (!q8) {
-        const uint16_t* base =
-            e >= 0 ? a.L.dn + (size_t)e * a.d.dn_stride() : a.L.sdn + (size_t)(-1 - e) * a.d.dn_stride();
-        const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)ht * nc * 64;
-        const int cpw = nc / kWaves;
-        tile_stream<N, false>(t, wave * cpw, (wave + 1) * cpw, s.as, xoff, acc);
-    } else {
-        const int ncq = F / 16;
-        const u32x4* t = reinterpret_cast<const u32x4*>(a.L.dn_q8 + (size_t)e * a.d.dn_stride()) + (size_t)ht * ncq * 64;
-        const int cpw = ncq / kWaves;
-        tile_stream<N, true>(t, wave * cpw, (wave + 1) * cpw, s.as, xoff, acc);
-    }
+    if (!q8) tb.run(s.as, xoff, acc);
+    else tq.run(s.as, xoff, acc);
     reduce_waves<N>(s.red, acc, N);
     if (wave == 0) {
         const int h = ht * 64 + lane;
@@ -554,7 +760,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
                 const int q = e < 0 ? sl : a.d.n_shared + rank[j];
                 float y = s.red[j * 64 + lane];
                 if (q8) y = y * scale;
-                st_sync(&a.ypart[((size_t)tok[j] * kq + q) * H + h], y);
+                st_tag(&a.ypart[((size_t)tok[j] * kq + q) * H + h], a.epoch, __float_as_uint(y));
             }
         }
     }
@@ -571,26 +777,64 @@ __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int
     else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank);
 }
 
-// Combine one output element: (out or 0) + shared terms + gate * routed terms, fixed order.
-__device__ __forceinline__ void combine_elem(const ExpertArgs& a, int t, int h) {
-    const int H = a.d.H, k = a.d.k, kq = a.d.n_shared + a.d.k;
-    const size_t o = (size_t)t * H + h;
-    float acc = a.accumulate ? a.out[o] : 0.f;
-    for (int q = 0; q < a.n_shared; q++) acc = acc + ld_sync(&a.ypart[((size_t)t * kq + q) * H + h]);
-    for (int r = 0; r < a.keep; r++)
-        if (ld_sync(&a.ids[t * k + r]) >= 0)
-            acc = fmaf(ld_sync(&a.gates[t * k + r]), ld_sync(&a.ypart[((size_t)t * kq + a.d.n_shared + r) * H + h]), acc);
-    a.out[o] = acc;
+// Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
+// routed terms in rank order (ranks with id -1 produced no output).  The down outputs are polled (tagged words).
+__device__ __forceinline__ void combine_tile(const ExpertArgs& a, const lds_RouteTab* rt, int ht) {
+    const int H = a.d.H, k = a.d.k, S = a.d.n_shared, kq = S + k;
+    for (int i = threadIdx.x; i < a.T * 64; i += blockDim.x) {
+        const int t = i / 64, h = ht * 64 + i % 64;
+        const uint64_t* yp = a.ypart + (size_t)t * kq * H + h;  // + q * H
+        uint64_t w[kMaxShared + kMaxTopk];
+        auto yptr = [&](int q) { return yp + (size_t)q * H; };
+        auto ylive = [&](int q) {
+            return q < kq && (q < S ? q < a.n_shared : (q - S < a.keep && rt->id[t * k + q - S] >= 0));
+        };
+#pragma unroll
+        for (int q = 0; q < kMaxShared + kMaxTopk; q++)  // every live term's load issued before any use
+            if (ylive(q)) w[q] = ld_sync(yptr(q));
+        settle(w, yptr, ylive, a.epoch, a.err);
+        const size_t o = (size_t)t * H + h;
+        float acc = a.accumulate ? a.out[o] : 0.f;
+#pragma unroll
+        for (int q = 0; q < kMaxShared + kMaxTopk; q++) {  // q < S: shared expert q; else rank q - S
+            if (q >= kq) continue;
+            if (q < S) {
+                if (q < a.n_shared) acc = acc + __uint_as_float((unsigned)w[q]);
+            } else if (q - S < a.keep && rt->id[t * k + q - S] >= 0) {
+                acc = fmaf(rt->gate[t * k + q - S], __uint_as_float((unsigned)w[q]), acc);
+            }
+        }
+        a.out[o] = acc;
+    }
 }
+
+// One slot of this workgroup's routing table.
+template <int NT>
+struct SlotRt {
+    int expert, ntok, pair0;
+    int tok[NT], rank[NT];
+    __device__ __forceinline__ void load(const lds_RouteTab* rt, int sl, int n_shared, int keep) {
+        expert = rt->slot_e[sl];
+        ntok = rt->slot_n[sl];
+        pair0 = rt->slot_pair[sl];
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int p = j < ntok ? rt->slot_p[sl][j] : 0;  // entries past ntok: keep indices in range
+            tok[j] = sl < n_shared ? p : p / keep;
+            rank[j] = sl < n_shared ? -1 : p % keep;
+        }
+    }
+};
 
 // Coherent snapshot of one slot of the table the route unit published.
 template <int NT>
 struct SlotView {
-    int expert, ntok;
+    int expert, ntok, pair0;
     int tok[NT], rank[NT];
     __device__ __forceinline__ void load(const Slots* sp, int sl) {  // independent loads: one round trip
         expert = ld_sync(&sp->expert[sl]);
         ntok = ld_sync(&sp->ntok[sl]);
+        pair0 = ld_sync(&sp->pair[sl]);
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             tok[j] = ld_sync(&sp->tok[sl][j]);
@@ -602,190 +846,219 @@ struct SlotView {
     }
 };
 
-// Publish this workgroup's coherent stores, then count the unit as done.
-__device__ __forceinline__ void signal_add(unsigned* p, unsigned v) {
-    wait_own_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Poll with relaxed agent-scope loads; after the barrier the workgroup reads the producers' data with ld_sync.
-__device__ __forceinline__ void wait_ge(unsigned* p, unsigned target, unsigned* err, uint64_t* stamp = nullptr) {
-    if (threadIdx.x == 0) {
-        unsigned n = 0;
-        while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(2);
-            ++n;
-            // give up after kSpinLimit polls, or at once when another wait of this launch already gave up
-            if (n > kSpinLimit || ((n & 255) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-        if (stamp) *stamp = __builtin_amdgcn_s_memrealtime();
-    }
-    __syncthreads();
-}
-
-
-
-// After a down unit of tile ht (live or skipped), count it; the last of the tile's maxs units combines the tile.
-__device__ __forceinline__ void down_done_combine(const ExpertArgs& a, Sync* sy, int ht) {
-    __shared__ int s_last;
-    wait_own_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(&sy->d_done[ht * kSyncPad], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (unsigned)(a.maxs - 1);
-    __syncthreads();
-    if (s_last)  // every down unit of this tile has published its partial outputs
-        for (int i = threadIdx.x; i < a.T * 64; i += blockDim.x) combine_elem(a, i / 64, ht * 64 + i % 64);
-    __syncthreads();
-}
-
-// At kernel exit the last workgroup clears the counters for the next launch on this context.
-__device__ __forceinline__ void exit_and_reset(Sync* sy) {
-    __shared__ int s_last;
-    wait_own_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(&sy->exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 gridDim.x - 1;
-    __syncthreads();
-    if (s_last) {
-        for (int i = threadIdx.x; i < kMaxSlots; i += blockDim.x) st_sync(&sy->gu_done[i * kSyncPad], 0u);
-        for (int i = threadIdx.x; i < kMaxHTiles; i += blockDim.x) st_sync(&sy->d_done[i * kSyncPad], 0u);
-        if (threadIdx.x == 0) {
-            st_sync(&sy->router_done, 0u);
-            st_sync(&sy->route_ready, 0u);
-            st_sync(&sy->next_unit, 0u);
-            st_sync(&sy->exit_count, 0u);
-        }
-    }
-}
-
 // ====================================================================================================================
-// Unfused path: one kernel per phase (stream order provides the dependencies).
+// Unfused path: one kernel per phase (stream order provides the dependencies; the tagged reads succeed at once).
 __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T, const uint16_t* __restrict__ x,
-                                                     float* __restrict__ logits) {
+                                                     uint64_t* __restrict__ logits, float* __restrict__ logits_out,
+                                                     unsigned epoch) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
-    stage_x(s, x, T, d.H);
-    if (T <= 1) router_unit<1>(s, L.wr, blockIdx.x * kWaves, d.E, d.H, T, logits);
-    else if (T <= 4) router_unit<4>(s, L.wr, blockIdx.x * kWaves, d.E, d.H, T, logits);
-    else router_unit<kMaxTokens>(s, L.wr, blockIdx.x * kWaves, d.E, d.H, T, logits);
+    const int e0 = blockIdx.x * kWaves;
+    if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
+    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
+    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
 }
 
 __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
-                                                         int do_topk, const float* __restrict__ logits,
-                                                         int32_t* __restrict__ ids, float* __restrict__ gates,
-                                                         Slots* __restrict__ slots) {
-    extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, 0, T, d.H, d.F, d.E);
-    route_unit(s, logits, L.bias, T, d.E, d.k, keep, n_shared, do_topk, ids, gates, slots);
+                                                         int do_topk, const uint64_t* __restrict__ logits,
+                                                         unsigned epoch, unsigned* err, int32_t* __restrict__ ids,
+                                                         float* __restrict__ gates, Slots* __restrict__ slots) {
+    __shared__ RouteTab rt_mem;
+    __shared__ __align__(16) unsigned char scr_mem[kRouteScratchBytes];
+    lds_RouteTab* rt = (lds_RouteTab*)&rt_mem;
+    route_local(rt, (LDS_AS unsigned char*)scr_mem, logits, epoch, err, L.bias, ids, gates, T, d.E, d.k, keep, n_shared,
+                do_topk);
+    route_publish(rt, T, d.k, keep, n_shared, do_topk, ids, gates, slots);
 }
 
 template <int NT>
-__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
-    const int ntile = a.d.F / 32;
-    const int sl = blockIdx.x / ntile, tile = blockIdx.x % ntile;
-    if (sl >= ld_sync(&a.slots->nslot) || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
+    if (blockIdx.x == 0 && threadIdx.x < 2) st_sync(&sy->next_unit[threadIdx.x * kSyncPad], 0u);
+    const int ntile = a.d.F / 32, g = ntile * a.kp;
+    const int sl = blockIdx.x / g, tile = (blockIdx.x % g) / a.kp, kpi = blockIdx.x % a.kp;
+    if (sl >= a.slots->nslot || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
     SlotView<NT> v;
     v.load(a.slots, sl);
     stage_x(s, a.x, a.T, a.d.H);
-    gateup_unit<NT>(s, a, sl, tile, v.expert, v.ntok, v.tok);
+    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0);
+}
+
+// Routing table of the combine, from the published slot table.
+__device__ __forceinline__ void load_combine_table(lds_RouteTab* rt, const Slots* sp, int T, int k) {
+    for (int p = threadIdx.x; p < T * k; p += blockDim.x) {
+        rt->id[p] = sp->vid[p];
+        rt->gate[p] = sp->vgate[p];
+    }
+    __syncthreads();
 }
 
 template <int NT>
-__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a, Sync* sy) {
+__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
+    __shared__ RouteTab rt_mem;
+    lds_RouteTab* rt = (lds_RouteTab*)&rt_mem;
     const Lds s = lds_carve(lds_raw, 0, NT, a.d.H, a.d.F, a.d.E);
     const int nht = a.d.H / 64;
     const int sl = blockIdx.x / nht, ht = blockIdx.x % nht;
-    if (sl < ld_sync(&a.slots->nslot) && (sl >= a.d.n_shared || sl < a.n_shared)) {  // else unused / left out
+    if (sl < a.slots->nslot && (sl >= a.d.n_shared || sl < a.n_shared)) {  // else unused / left out
         SlotView<NT> v;
         v.load(a.slots, sl);
         down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
     }
-    down_done_combine(a, sy, ht);
-    exit_and_reset(sy);
+    if (sl == a.maxs - 1) {  // the last slot's unit of each tile combines it
+        load_combine_table(rt, a.slots, a.T, a.d.k);
+        combine_tile(a, rt, ht);
+    }
 }
-
 
 // ====================================================================================================================
 // Fused path: one persistent kernel walks the unit list
-//   [router units][route unit][shared gate|up][routed gate|up][down, slot-major]
-// through a work queue: a global counter hands out unit indices in ascending order, and each workgroup fetches its
-// next index while it works on the current one.  A unit waits only on units of smaller index; the smallest
-// unfinished unit is therefore always some running workgroup's current unit and can proceed, so the grid needs no
-// co-residency guarantee (a plain launch).  Every wait is also bounded by kSpinLimit.  The last down unit of each
-// 64-row tile combines that tile; the last workgroup to finish clears the counters for the next launch.
+//   [router units][route publisher][shared slots' gate|up parts][shared slots' downs]
+//   [routed gate|up and down blocks][remaining routed downs]
+// A slot's gate|up block holds its F/32 tiles x kp K parts (parts of a tile adjacent, the finishing part last); its
+// down block holds its H/64 down tiles.  Routed slot s's gate|up block is followed by routed slot (s - lag)'s down
+// block, so a down unit is handed out about lag blocks after the gate|up units it reads.  Workgroup b runs units b and grid + b
+// first; further units come from a work queue (a counter handed out in ascending order, fetched while the current
+// unit runs).  A unit only ever waits for data produced by units of smaller index, and the smallest unfinished unit
+// always has a running workgroup on it, so the grid needs no co-residency guarantee (a plain launch); every wait is
+// also bounded.  Each
+// workgroup that needs the routing computes it into its own shared-memory table from the tagged logits; the
+// publisher unit only writes ids / gates / the slot table for the caller.  The last slot's down unit of each 64-row
+// tile combines that tile.
+struct UnitRef {
+    int kind;  // 0 router, 1 publisher, 2 gate|up part, 3 down tile
+    int sl, idx;
+};
+__device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int g, int nht, int lag) {
+    if (u < uR) return {0, 0, u};
+    u -= uR;
+    if (u < 1) return {1, 0, 0};
+    u -= 1;
+    if (u < S * g) return {2, u / g, u % g};  // shared slots' gate|up parts
+    u -= S * g;
+    if (u < S * nht) return {3, u / nht, u % nht};  // shared slots' downs (no routing needed)
+    u -= S * nht;
+    const int Mr = M - S;               // routed slots S .. M - 1, numbered r = slot - S below
+    const int n0 = min(lag, Mr);        // gate|up-only blocks: r = 0 .. n0 - 1
+    if (u < n0 * g) return {2, S + u / g, u % g};
+    u -= n0 * g;
+    const int n1 = max(0, Mr - lag);    // paired steps i: gate|up of r = lag + i, then down of r = i
+    if (u < n1 * (g + nht)) {
+        const int i = u / (g + nht), w = u % (g + nht);
+        return w < g ? UnitRef{2, S + lag + i, w} : UnitRef{3, S + i, w - g};
+    }
+    u -= n1 * (g + nht);
+    return {3, S + n1 + u / nht, u % nht};  // downs of the last routed slots
+}
+
 template <int NT>
 __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
+    __shared__ RouteTab rt_mem;
+    __shared__ int s_unit, s_routed, s_staged;
+    lds_RouteTab* rt = (lds_RouteTab*)&rt_mem;
     const ExpertArgs& a = f.e;
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     Sync* sy = f.sync;
-    const int H = a.d.H, F = a.d.F;
-    const int ntile = F / 32, nht = H / 64;
+    const int H = a.d.H, F = a.d.F, S = a.d.n_shared;
+    const int ntile = F / 32, nht = H / 64, g = ntile * a.kp;
     const int maxs = a.maxs;
-    const int uR = f.nR, uRoute = uR + 1, uGUs = uRoute + a.d.n_shared * ntile, uGU = uRoute + maxs * ntile;
-    const int uEnd = uGU + maxs * nht;
-    __shared__ int s_unit;
-    if (threadIdx.x == 0) s_unit = (int)__hip_atomic_fetch_add(&sy->next_unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    stage_x(s, a.x, a.T, H);  // ends with a barrier: s_unit is visible
-    uint64_t t_start = 0;
-    for (int u = s_unit; u < uEnd;) {
-        int next = 0;
-        if (threadIdx.x == 0) {  // fetch the next unit now; its latency hides behind this unit's work
-            next = (int)__hip_atomic_fetch_add(&sy->next_unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (f.trace) {
-                t_start = __builtin_amdgcn_s_memrealtime();
-                f.trace[(size_t)u * 4 + 1] = 0;
-            }
+    const int uEnd = fused_units(f.nR, maxs, F, H, a.kp);
+    unsigned* queue = &sy->next_unit[(a.epoch & 1u) * kSyncPad];
+    if (threadIdx.x == 0) {
+        s_routed = 0;
+        s_staged = 0;
+        if (blockIdx.x == 0) st_sync(&sy->next_unit[((a.epoch & 1u) ^ 1u) * kSyncPad], 0u);  // the next launch's head
+    }
+    __syncthreads();
+    auto ensure_routed = [&]() {
+        if (!s_routed) {
+            route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
+                        a.d.E, a.d.k, a.keep, S, f.do_topk);
+            if (threadIdx.x == 0) s_routed = 1;
+            __syncthreads();
         }
-        if (u < uR) {
-            router_unit<NT>(s, a.L.wr, u * kWaves, a.d.E, H, a.T, f.logits);
-            signal_add(&sy->router_done, 1);
-        } else if (u < uRoute) {
-            if (uR) wait_ge(&sy->router_done, (unsigned)uR, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
-            route_unit(s, f.logits, a.L.bias, a.T, a.d.E, a.d.k, a.keep, a.d.n_shared, f.do_topk, a.ids, a.gates,
-                       a.slots);
-            signal_add(&sy->route_ready, 1);
-        } else if (u < uGU) {
-            const int sl = (u - uRoute) / ntile, tile = (u - uRoute) % ntile;
-            if (u < uGUs) {  // shared slot: all tokens in order, no routing dependency
+    };
+    auto ensure_staged = [&]() {
+        if (!s_staged) {
+            stage_x(s, a.x, a.T, H);
+            if (threadIdx.x == 0) s_staged = 1;
+            __syncthreads();
+        }
+    };
+    uint64_t t_start = 0;
+    // Units b and grid + b are this workgroup's first two (no queue traffic while every workgroup starts at once);
+    // from the second unit on, the index after the current one is fetched from the queue while the current one runs.
+    const int grid = (int)gridDim.x;
+    for (int u = blockIdx.x, round = 0; u < uEnd; round++) {
+        int next = 0;
+        if (threadIdx.x == 0) {
+            if (round == 0) next = grid + (int)blockIdx.x;
+            else next = 2 * grid + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
+        }
+        const UnitRef ur = decode_unit(u, f.nR, S, maxs, g, nht, f.lag);
+        uint64_t t_ready = 0;
+        if (ur.kind == 0) {
+            const bool stage = !s_staged;
+            router_unit<NT>(s, a.L.wr, ur.idx * kWaves, a.d.E, H, a.T, f.logits, nullptr, a.epoch,
+                            stage ? a.x : nullptr);
+            if (stage && threadIdx.x == 0) s_staged = 1;
+        } else if (ur.kind == 1) {
+            ensure_routed();
+            if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
+            route_publish(rt, a.T, a.d.k, a.keep, S, f.do_topk, a.ids, a.gates, a.slots);
+        } else if (ur.kind == 2) {
+            const int sl = ur.sl, tile = ur.idx / a.kp, kpi = ur.idx % a.kp;
+            ensure_staged();  // x first: its load overlaps the wait for the routing
+            if (sl < S) {  // shared slot: all tokens in order, no routing dependency
+                if (f.shared_waits) ensure_routed();  // optional: keep the memory system quiet while routing
                 if (sl < a.n_shared) {
                     int tok[NT];
 #pragma unroll
                     for (int j = 0; j < NT; j++) tok[j] = j;
-                    gateup_unit<NT>(s, a, sl, tile, -1 - sl, a.T, tok);
+                    gateup_unit<NT>(s, a, sl, tile, kpi, -1 - sl, a.T, tok, sl * a.T);
                 }
             } else {
-                wait_ge(&sy->route_ready, 1, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
-                if (sl < ld_sync(&a.slots->nslot)) {
-                    SlotView<NT> v;
-                    v.load(a.slots, sl);
-                    gateup_unit<NT>(s, a, sl, tile, v.expert, v.ntok, v.tok);
+                ensure_routed();
+                if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
+                if (sl < rt->nslot) {
+                    SlotRt<NT> v;
+                    v.load(rt, sl, S, a.keep);
+                    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0);
                 }
             }
-            signal_add(&sy->gu_done[sl * kSyncPad], 1);
         } else {
-            const int sl = (u - uGU) / nht, ht = (u - uGU) % nht;
-            wait_ge(&sy->route_ready, 1, &sy->err);
-            const bool live = sl < ld_sync(&a.slots->nslot) && (sl >= a.d.n_shared || sl < a.n_shared);
-            if (live) {
-                SlotView<NT> v;
-                v.load(a.slots, sl);
-                wait_ge(&sy->gu_done[sl * kSyncPad], (unsigned)ntile, &sy->err, f.trace ? f.trace + (size_t)u * 4 + 1 : nullptr);
-                down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
+            const int sl = ur.sl, ht = ur.idx;
+            if (sl < S) {  // shared slot: all tokens in order, no routing dependency
+                if (sl < a.n_shared) {
+                    int tok[NT], rank[NT];
+#pragma unroll
+                    for (int j = 0; j < NT; j++) {
+                        tok[j] = j;
+                        rank[j] = -1;
+                    }
+                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank);
+                }
+            } else {
+                ensure_routed();
+                if (sl < rt->nslot) {
+                    SlotRt<NT> v;
+                    v.load(rt, sl, S, a.keep);
+                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
+                }
             }
-            down_done_combine(a, sy, ht);
+            if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
+            if (sl == maxs - 1) {  // the last slot's unit of each tile combines it
+                ensure_routed();
+                combine_tile(a, rt, ht);
+            }
         }
         if (f.trace && threadIdx.x == 0) {
             f.trace[(size_t)u * 4 + 0] = t_start;
+            f.trace[(size_t)u * 4 + 1] = t_ready;
             f.trace[(size_t)u * 4 + 2] = __builtin_amdgcn_s_memrealtime();
             f.trace[(size_t)u * 4 + 3] = blockIdx.x;
         }
@@ -794,7 +1067,6 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         __syncthreads();
         u = s_unit;
     }
-    exit_and_reset(sy);
 }
 
 // --------------------------------------------------------------------------------------------------------------------
@@ -948,6 +1220,10 @@ __global__ void synth_tiled_kernel(uint64_t key_g, uint64_t key_u, uint64_t key_
     }
 }
 
+__global__ void zero_kernel(uint64_t* __restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) dst[i] = 0;
+}
+
 __global__ void synth_fill_kernel(u32x4* __restrict__ dst, uint64_t nchunk, uint64_t key, uint64_t start, float c) {
     const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q < nchunk) dst[q] = synth_chunk(key, start + q * 8, c);
@@ -964,63 +1240,62 @@ static hipError_t set_lds(const void* fn, size_t lds) {
 
 static int nt_bucket(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
-hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, float* logits, hipStream_t st) {
+hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, uint64_t* logits,
+                         float* logits_out, unsigned epoch, hipStream_t st) {
     const size_t lds = lds_bytes(T, 1, d.H, d.F, d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&router_kernel), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kWaves)), dim3(256), lds, st, L, d, T, x, logits);
+    hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kWaves)), dim3(256), lds, st, L, d, T, x, logits, logits_out,
+                       epoch);
     return hipGetLastError();
 }
 
 hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
-                             const float* logits, int32_t* ids, float* gates, Slots* slots, hipStream_t st) {
-    const size_t lds = lds_bytes(0, T, d.H, d.F, d.E);
-    hipError_t e = set_lds(reinterpret_cast<const void*>(&topk_group_kernel), lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), lds, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, logits,
-                       ids, gates, slots);
+                             const uint64_t* logits, unsigned epoch, unsigned* err, int32_t* ids, float* gates,
+                             Slots* slots, hipStream_t st) {
+    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), 0, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, logits,
+                       epoch, err, ids, gates, slots);
     return hipGetLastError();
 }
 
 template <int NT>
-static hipError_t gateup_nt(const ExpertArgs& ea, hipStream_t st) {
+static hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     const int maxs = ea.maxs;
     const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&gateup_kernel<NT>), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gateup_kernel<NT>, dim3(maxs * (ea.d.F / 32)), dim3(256), lds, st, ea);
+    hipLaunchKernelGGL(gateup_kernel<NT>, dim3(maxs * (ea.d.F / 32) * ea.kp), dim3(256), lds, st, ea, sy);
     return hipGetLastError();
 }
 
 template <int NT>
-static hipError_t down_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
+static hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
     const size_t lds = lds_bytes(0, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&down_kernel<NT>), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(down_kernel<NT>, dim3(ea.maxs * (ea.d.H / 64)), dim3(256), lds, st, ea, sy);
+    hipLaunchKernelGGL(down_kernel<NT>, dim3(ea.maxs * (ea.d.H / 64)), dim3(256), lds, st, ea);
     return hipGetLastError();
 }
 
-hipError_t launch_gateup(const ExpertArgs& ea, hipStream_t st) {
+hipError_t launch_gateup(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     switch (nt_bucket(ea.T)) {
-        case 1: return gateup_nt<1>(ea, st);
-        case 2: return gateup_nt<2>(ea, st);
-        case 4: return gateup_nt<4>(ea, st);
-        case 8: return gateup_nt<8>(ea, st);
-        default: return gateup_nt<16>(ea, st);
+        case 1: return gateup_nt<1>(ea, sy, st);
+        case 2: return gateup_nt<2>(ea, sy, st);
+        case 4: return gateup_nt<4>(ea, sy, st);
+        case 8: return gateup_nt<8>(ea, sy, st);
+        default: return gateup_nt<16>(ea, sy, st);
     }
 }
 
-hipError_t launch_down(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
+hipError_t launch_down(const ExpertArgs& ea, hipStream_t st) {
     switch (nt_bucket(ea.T)) {
-        case 1: return down_nt<1>(ea, sy, st);
-        case 2: return down_nt<2>(ea, sy, st);
-        case 4: return down_nt<4>(ea, sy, st);
-        case 8: return down_nt<8>(ea, sy, st);
-        default: return down_nt<16>(ea, sy, st);
+        case 1: return down_nt<1>(ea, st);
+        case 2: return down_nt<2>(ea, st);
+        case 4: return down_nt<4>(ea, st);
+        case 8: return down_nt<8>(ea, st);
+        default: return down_nt<16>(ea, st);
     }
 }
-
 
 template <int NT>
 static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
@@ -1042,7 +1317,7 @@ static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid
     int per_cu = c_per_cu, ncu = c_ncu;
     if (wg_per_cu > 0 && wg_per_cu < per_cu) per_cu = wg_per_cu;
     if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const int units = f.nR + 1 + f.e.maxs * (f.e.d.F / 32) + f.e.maxs * (f.e.d.H / 64);
+    const int units = fused_units(f.nR, f.e.maxs, f.e.d.F, f.e.d.H, f.e.kp);
     int grid = ncu * per_cu;
     if (grid > units) grid = units;
     if (grid_out) *grid_out = grid;
@@ -1123,6 +1398,14 @@ uint64_t synth_key(uint64_t seed, uint64_t tensor_id) { return mix64(seed * 0xD1
 bool kernels_available() {
     hipFuncAttributes attr;
     return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&router_kernel)) == hipSuccess;
+}
+
+hipError_t launch_zero(uint64_t* dst, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n);
+    return hipGetLastError();
 }
 
 }  // namespace moe

@@ -378,3 +378,69 @@ def test_fused_varied_calls_match_unfused(solar):
             np.testing.assert_array_equal(f.view(np.uint32), u.view(np.uint32))
     finally:
         tier.set_option(OPT_FUSED, 1)
+
+
+# ------------------------------------------------------------------------------------------------ K split / queue lag
+@pytest.mark.parametrize("kp", [2, 4])
+def test_tiny_ksplit_matches_oracle_and_paths(tiny, kp):
+    """Split gate|up tiles (K parts reduced in fixed order by the tile's last part): within the bars of the oracle,
+    and the fused and one-kernel-per-phase paths give identical bits for the same K split."""
+    from moe_gpu import OPT_FUSED, OPT_KSPLIT
+    tier, hl = tiny
+    rng = np.random.default_rng(120 + kp)
+    try:
+        for T in (1, 3, 16):
+            say(f"tiny K split {kp} T={T}")
+            x = random_x(T, TINY.H, rng)
+            ref = oracle_layer(hl, x)
+            tier.set_option(OPT_KSPLIT, kp)
+            tier.set_option(OPT_FUSED, 1)
+            of, idf, gf = tier.layer(0, x)
+            tier.set_option(OPT_FUSED, 0)
+            ou, idu, gu = tier.layer(0, x)
+            check_route(idf, gf, ref, TINY.k)
+            np.testing.assert_array_equal(idf, idu)
+            np.testing.assert_array_equal(of.view(np.uint32), ou.view(np.uint32))
+            r = assert_layer_close(of, ref["out"])
+            assert r["rel_l2"] < 1e-4, r
+    finally:
+        tier.set_option(OPT_FUSED, 1)
+        tier.set_option(OPT_KSPLIT, 0)
+
+
+def test_solar_queue_lag_does_not_change_bits(solar):
+    """The fused queue order (lag of down blocks) only reorders work: identical bits for every lag and grid size."""
+    from moe_gpu import OPT_LAG, OPT_SHARED_WAITS, OPT_WG_PER_CU
+    tier, hl = solar
+    x = random_x(3, SOLAR.H, np.random.default_rng(130))
+    say("solar queue lag / grid / shared-wait sweep T=3")
+    base, _, _ = tier.layer(0, x)
+    try:
+        for lag in (1, 3, 7, 40):
+            for wg in (1, 2):
+                tier.set_option(OPT_LAG, lag)
+                tier.set_option(OPT_WG_PER_CU, wg)
+                tier.set_option(OPT_SHARED_WAITS, (lag + wg) % 2)
+                o, _, _ = tier.layer(0, x)
+                np.testing.assert_array_equal(o.view(np.uint32), base.view(np.uint32))
+    finally:
+        tier.set_option(OPT_LAG, 0)
+        tier.set_option(OPT_WG_PER_CU, 1)
+        tier.set_option(OPT_SHARED_WAITS, 0)
+
+
+@pytest.mark.parametrize("kp", [1, 2])
+def test_solar_ksplit_within_bars(solar, kp):
+    """Solar layer with other K splits than the automatic one (4 parts at H=4096): same ids, outputs within bars."""
+    from moe_gpu import OPT_KSPLIT
+    tier, hl = solar
+    x = random_x(1, SOLAR.H, np.random.default_rng(140 + kp))
+    say(f"solar K split {kp}")
+    ref = oracle_layer(hl, x)
+    try:
+        tier.set_option(OPT_KSPLIT, kp)
+        out, ids, gates = tier.layer(0, x)
+    finally:
+        tier.set_option(OPT_KSPLIT, 0)
+    check_route(ids, gates, ref, SOLAR.k)
+    assert_layer_close(out, ref["out"])
