@@ -93,6 +93,20 @@ def cpu_baseline(w: Workload, budget_s: float = 12.0) -> dict | None:
                       f"{ne}-expert pool + router GEMV/top-k), median; {'cpu_kern.c ck_gemv+ck_moe3' if kind == 'reference' else 'scalar restatement'}"}
 
 
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on bench workload `workload` from the committed rocprofv3 counter summary
+    (profiles/<kernel>_<workload>_traffic.txt, line `traffic_bytes_per_launch: N`), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,10 +116,13 @@ def main():
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after timing, run 5 plain device copies of MIB MiB (reference kernel for rocprof "
+                         "FETCH_SIZE / WRITE_SIZE scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the expert tier shards by expert across "
-              "GPUs only by design, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the expert tier would shard by expert "
+              "across GPUs, which is designed but not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -157,6 +174,17 @@ def main():
     achieved = avg_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"{ms_per_step * 1e3:.2f} us/step (events {ev_ms / K * 1e3:.2f}), {achieved:.0f} GB/s algorithmic")
 
+    # per-call latency distribution: one event pair around every call (hipEvents on the call's stream)
+    log("per-call event pass")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    for i in range(K):
+        evs[i][0].record(stream)
+        tier.layer_dev(i % L, T, xs[i % P], out, ids[i], gates[i], keep=w.keep, flags=flags)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    per_call = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    median_us, p90_us = per_call[len(per_call) // 2], per_call[min(len(per_call) - 1, int(0.9 * len(per_call)))]
+
     roofline = None
     kernels = None
     if not args.no_profile:
@@ -180,9 +208,22 @@ def main():
             k_bytes = float(np.mean([u * per_expert_gu + w.n_shared * 2 * w.F * w.H * 2 for u in distinct]))
         k_avg_s = k_ms / k_n * 1e-3
         k_gbps = k_bytes / k_avg_s / 1e9
+        traffic = measured_traffic(k_name, args.workload)
         roofline = {"kernel": k_name, "bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS,
-                    "unit": "GB/s", "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                     "bytes_per_launch": int(k_bytes), "avg_us": round(k_avg_s * 1e6, 2)}
+
+    if args.copy_calibration > 0:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {args.copy_calibration} MiB")
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline and w.T == 1:
@@ -195,6 +236,7 @@ def main():
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8w-bf16" if w.int8 else "bf16", "data": "synthetic (seeded, weights ~N(0,0.02), x ~N(0,1))",
         "achieved_TBps": round(achieved / 1e3, 3), "hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "median_us_per_call": round(median_us, 2), "p90_us_per_call": round(p90_us, 2),
         "algorithmic_bytes_per_step": int(avg_bytes), "event_ms_per_step": round(ev_ms / K, 5),
         "decode_layer_calls_per_s": round(1e3 / ms_per_step, 1),
         "config": {"workload": w.name, "H": w.H, "F": w.F, "E": w.E, "topk": w.k, "n_shared": w.n_shared,
