@@ -125,7 +125,8 @@ uint64_t moe_gpu_synth_key(uint64_t seed, uint64_t tensor_id);
 int moe_gpu_enable_timing(moe_gpu* ctx, int on);
 int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 /* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent kernel that walks router
- * rows, top-k/grouping, gate|up tile parts and down tiles (a work queue with on-device dependency counters); 0 runs
+ * rows, top-k/grouping, gate|up tile parts and down tiles (a work queue; cross-workgroup values are epoch-tagged words
+ * that their consumers poll); 0 runs
  * one kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in
  * workgroups per CU (default 1; 0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused
  * launch.  MOE_GPU_OPT_KSPLIT: K parts per gate|up tile, 1, 2 or 4 (0 = automatic: about 256 KiB of weights per part); it
@@ -141,7 +142,7 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
- * {start, dependencies met (0 if none), end, workgroup} in the 100 MHz s_memrealtime clock; read_trace copies the
+ * {start, inputs ready (0 if the unit has none), end, workgroup} in the 100 MHz s_memrealtime clock; read_trace copies the
  * last launch's records (4 uint64 per unit, in the fused kernel's unit order). */
 int moe_gpu_trace_units(moe_gpu* ctx, int on);
 int moe_gpu_read_trace(moe_gpu* ctx, uint64_t* buf, int max_units, int* units);
