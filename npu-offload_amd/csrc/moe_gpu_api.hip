@@ -75,6 +75,7 @@ struct moe_gpu {
     int shared_waits = 0;  // MOE_GPU_OPT_SHARED_WAITS
     uint64_t* d_gpart = nullptr;    // tagged split gate|up partial sums
     unsigned epoch = 0;             // tag of the last call (tags are never 0)
+    unsigned fused_launches = 0;    // selects the fused kernel's work-queue head
     size_t act_bytes = 0, ypart_bytes = 0, gpart_bytes = 0, logits_tag_bytes = 0;
     // per-kernel profiling: event pairs recorded around each launch, resolved on read
     bool profiling = false;
@@ -321,6 +322,7 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
         f.do_topk = do_topk ? 1 : 0;
         f.trace = c->d_trace;
         f.lag = c->lag > 0 ? c->lag : 8;
+        f.phase = (int)(c->fused_launches++ & 1u);
         f.shared_waits = c->shared_waits;
         c->trace_units = moe::fused_units(f.nR, a.maxs, c->d.F, c->d.H, a.kp);
         LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->stream, &c->last_grid));
@@ -780,8 +782,9 @@ int moe_gpu_trace_units(moe_gpu* c, int on) {
     if (on && !c->d_trace) {
         const size_t units = (size_t)moe::fused_units((c->d.E + moe::kWaves - 1) / moe::kWaves,
                                                       c->d.n_shared + c->d.max_t * c->d.k, c->d.F, c->d.H, 4);
-        if ((rc = dev_alloc(c, (void**)&c->d_trace, units * 4 * sizeof(uint64_t), "unit trace"))) return rc;
-        HIPCHK(c, hipMemset(c->d_trace, 0, units * 4 * sizeof(uint64_t)));
+        const size_t bytes = units * moe::kTraceFields * sizeof(uint64_t);
+        if ((rc = dev_alloc(c, (void**)&c->d_trace, bytes, "unit trace"))) return rc;
+        HIPCHK(c, hipMemset(c->d_trace, 0, bytes));
     } else if (!on && c->d_trace) {
         HIPCHK(c, hipStreamSynchronize(c->stream));
         HIPCHK(c, hipFree(c->d_trace));
@@ -797,7 +800,7 @@ int moe_gpu_read_trace(moe_gpu* c, uint64_t* buf, int max_units, int* units) {
     if (!buf || !units) return fail(c, MOE_GPU_EINVAL, "NULL buffer");
     const int n = c->trace_units < max_units ? c->trace_units : max_units;
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    HIPCHK(c, hipMemcpy(buf, c->d_trace, (size_t)n * 4 * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    HIPCHK(c, hipMemcpy(buf, c->d_trace, (size_t)n * moe::kTraceFields * sizeof(uint64_t), hipMemcpyDeviceToHost));
     *units = n;
     return MOE_GPU_OK;
 }

@@ -82,14 +82,19 @@ struct ExpertArgs {
     unsigned* err;                            // set when a bounded wait gave up (sticky until the host clears it)
 };
 
-// Work-queue heads of the fused kernel.  A launch with epoch n hands out units from next_unit[n & 1] and clears
-// next_unit[(n + 1) & 1] for the next launch; each head sits in its own 128-byte line.
+// Work-queue heads of the fused kernel.  Fused launch n (the host counts them) hands out units from
+// next_unit[n & 1] and clears next_unit[(n + 1) & 1] for the next launch; the unfused path clears both.  Each head
+// sits in its own 128-byte line.
 constexpr int kSyncPad = 32;  // unsigneds per line
 struct Sync {
     unsigned err;  // set when a bounded wait gave up (sticky until the host clears it)
     unsigned pad0_[kSyncPad - 1];
     unsigned next_unit[2 * kSyncPad];
 };
+
+// Unit trace record (fused kernel, optional): start, inputs ready, end (100 MHz s_memrealtime ticks), workgroup,
+// aux (gate|up finishing part: sibling partials in; down unit: act rows staged; else 0), reserved.
+constexpr int kTraceFields = 6;
 
 struct FusedArgs {
     ExpertArgs e;
@@ -98,6 +103,7 @@ struct FusedArgs {
     uint64_t* trace;  // optional: per unit {start, dependencies met, end, workgroup} in 100 MHz realtime ticks
     int nR;         // router units (0 when the caller gives ids)
     int do_topk;
+    int phase;      // work-queue head of this launch (fused launch count & 1)
     int lag;        // queue order: routed slot s's down block follows routed slot (s + lag)'s gate|up block (lag >= 1)
     int shared_waits;  // 1: shared gate|up parts start only once the routing is known
 };

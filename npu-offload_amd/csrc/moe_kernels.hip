@@ -626,7 +626,7 @@ __device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int
 // publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
 template <int N>
 __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
-                                            const int* tok, int pair0) {
+                                            const int* tok, int pair0, uint64_t* stamp) {
     const int H = a.d.H, F = a.d.F, kp = a.kp, ntile = F / 32;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = H / 8;
@@ -668,6 +668,7 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
 #pragma unroll
             for (int j = 0; j < N; j++) {
                 settle(w[j], [&](int q) { return gptr(j, q); }, [&](int q) { return q < kp - 1; }, a.epoch, a.err);
+                if (stamp && j == 0 && lane == 0) *stamp = __builtin_amdgcn_s_memrealtime();
                 float v = 0.f;
 #pragma unroll
                 for (int q = 0; q < 3; q++) {
@@ -692,19 +693,19 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
 
 template <int NT>
 __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
-                                            const int* tok, int pair0) {
-    if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
-    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
-    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
-    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
-    else gateup_core<NT>(s, a, sl, tile, kpi, e, ntok, tok, pair0);
+                                            const int* tok, int pair0, uint64_t* stamp = nullptr) {
+    if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else gateup_core<NT>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
 }
 
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
 // slot and n_shared + rank for a routed one.
 template <int N>
 __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank) {
+                          const int* rank, uint64_t* stamp) {
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = F / 8;
@@ -741,6 +742,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
             if (aneed(m)) dst[i0 + m * (int)blockDim.x + (int)threadIdx.x] = (unsigned)w[m];
     }
     __syncthreads();
+    if (stamp && threadIdx.x == 0) *stamp = __builtin_amdgcn_s_memrealtime();
     int xoff[N];
 #pragma unroll
     for (int j = 0; j < N; j++) xoff[j] = j < ntok ? j * nc : 0;
@@ -769,12 +771,12 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
 
 template <int NT>
 __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank) {
-    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank);
-    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank);
-    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank);
-    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank);
-    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank);
+                          const int* rank, uint64_t* stamp = nullptr) {
+    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, stamp);
+    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
+    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
+    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
+    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, stamp);
 }
 
 // Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
@@ -875,7 +877,7 @@ template <int NT>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
-    if (blockIdx.x == 0 && threadIdx.x < 2) st_sync(&sy->next_unit[threadIdx.x * kSyncPad], 0u);
+    if (blockIdx.x == 0 && threadIdx.x < 2) st_sync(&sy->next_unit[threadIdx.x * kSyncPad], 0u);  // fused queue heads
     const int ntile = a.d.F / 32, g = ntile * a.kp;
     const int sl = blockIdx.x / g, tile = (blockIdx.x % g) / a.kp, kpi = blockIdx.x % a.kp;
     if (sl >= a.slots->nslot || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
@@ -966,11 +968,12 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     const int ntile = F / 32, nht = H / 64, g = ntile * a.kp;
     const int maxs = a.maxs;
     const int uEnd = fused_units(f.nR, maxs, F, H, a.kp);
-    unsigned* queue = &sy->next_unit[(a.epoch & 1u) * kSyncPad];
+    const int ph = f.phase & 1;
+    unsigned* queue = &sy->next_unit[ph * kSyncPad];
     if (threadIdx.x == 0) {
         s_routed = 0;
         s_staged = 0;
-        if (blockIdx.x == 0) st_sync(&sy->next_unit[((a.epoch & 1u) ^ 1u) * kSyncPad], 0u);  // the next launch's head
+        if (blockIdx.x == 0) st_sync(&sy->next_unit[(ph ^ 1) * kSyncPad], 0u);  // the next launch's head
     }
     __syncthreads();
     auto ensure_routed = [&]() {
@@ -1000,7 +1003,8 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
         }
         const UnitRef ur = decode_unit(u, f.nR, S, maxs, g, nht, f.lag);
-        uint64_t t_ready = 0;
+        uint64_t t_ready = 0, t_aux = 0;
+        uint64_t* aux = f.trace ? &t_aux : nullptr;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
             router_unit<NT>(s, a.L.wr, ur.idx * kWaves, a.d.E, H, a.T, f.logits, nullptr, a.epoch,
@@ -1019,7 +1023,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                     int tok[NT];
 #pragma unroll
                     for (int j = 0; j < NT; j++) tok[j] = j;
-                    gateup_unit<NT>(s, a, sl, tile, kpi, -1 - sl, a.T, tok, sl * a.T);
+                    gateup_unit<NT>(s, a, sl, tile, kpi, -1 - sl, a.T, tok, sl * a.T, aux);
                 }
             } else {
                 ensure_routed();
@@ -1027,7 +1031,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                 if (sl < rt->nslot) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
-                    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0);
+                    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, aux);
                 }
             }
         } else {
@@ -1040,14 +1044,14 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                         tok[j] = j;
                         rank[j] = -1;
                     }
-                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank);
+                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank, aux);
                 }
             } else {
                 ensure_routed();
                 if (sl < rt->nslot) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
-                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
+                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, aux);
                 }
             }
             if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
@@ -1057,15 +1061,18 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             }
         }
         if (f.trace && threadIdx.x == 0) {
-            f.trace[(size_t)u * 4 + 0] = t_start;
-            f.trace[(size_t)u * 4 + 1] = t_ready;
-            f.trace[(size_t)u * 4 + 2] = __builtin_amdgcn_s_memrealtime();
-            f.trace[(size_t)u * 4 + 3] = blockIdx.x;
+            uint64_t* tr = f.trace + (size_t)u * kTraceFields;
+            tr[0] = t_start;
+            tr[1] = t_ready;
+            tr[2] = __builtin_amdgcn_s_memrealtime();
+            tr[3] = blockIdx.x;
+            tr[4] = t_aux;
+            tr[5] = 0;
         }
         __syncthreads();  // the whole workgroup is done with unit u before s_unit changes
         if (threadIdx.x == 0) s_unit = next;
         __syncthreads();
-        u = s_unit;
+        u = __builtin_amdgcn_readfirstlane(s_unit);  // uniform: unit decoding stays in scalar registers
     }
 }
 

@@ -218,9 +218,9 @@ class MoeGpu:
         self._chk(self.L.moe_gpu_trace_units(self.h, 1 if on else 0))
 
     def read_trace(self) -> np.ndarray:
-        """[units, 4] uint64: start, dependencies met, end (100 MHz ticks), workgroup — of the last fused launch."""
+        """[units, 6] uint64: start, inputs ready, end (100 MHz ticks), workgroup, aux, 0 — of the last fused launch."""
         cap = 1 << 16
-        buf = np.zeros((cap, 4), np.uint64); n = C.c_int()
+        buf = np.zeros((cap, 6), np.uint64); n = C.c_int()
         self._chk(self.L.moe_gpu_read_trace(self.h, _p(buf), cap, C.byref(n)))
         return buf[: n.value].copy()
 

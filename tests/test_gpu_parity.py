@@ -444,3 +444,18 @@ def test_solar_ksplit_within_bars(solar, kp):
         tier.set_option(OPT_KSPLIT, 0)
     check_route(ids, gates, ref, SOLAR.k)
     assert_layer_close(out, ref["out"])
+
+
+def test_fused_calls_interleaved_with_route_calls(solar):
+    """Route-only calls between fused layer calls (they take call tags but run no fused kernel) must not disturb the
+    fused kernel's work queue: every layer call gives the first call's bits."""
+    tier, hl = solar
+    x = random_x(1, SOLAR.H, np.random.default_rng(150))
+    say("solar fused calls interleaved with route calls")
+    first, ids0, _ = tier.layer(0, x)
+    for pattern in ("r", "rr", "", "r", "rrr", ""):
+        for _ in pattern:
+            ids, _ = tier.route(0, x)
+            np.testing.assert_array_equal(ids, ids0)
+        again, _, _ = tier.layer(0, x)
+        np.testing.assert_array_equal(again.view(np.uint32), first.view(np.uint32))
