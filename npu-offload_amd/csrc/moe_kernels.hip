@@ -626,7 +626,7 @@ __device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int
 // publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
 template <int N>
 __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
-                                            const int* tok, int pair0, uint64_t* stamp) {
+                                            const int* tok, int pair0, uint64_t& stamp) {
     const int H = a.d.H, F = a.d.F, kp = a.kp, ntile = F / 32;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = H / 8;
@@ -668,7 +668,7 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
 #pragma unroll
             for (int j = 0; j < N; j++) {
                 settle(w[j], [&](int q) { return gptr(j, q); }, [&](int q) { return q < kp - 1; }, a.epoch, a.err);
-                if (stamp && j == 0 && lane == 0) *stamp = __builtin_amdgcn_s_memrealtime();
+                if (j == 0) stamp = __builtin_amdgcn_s_memrealtime();
                 float v = 0.f;
 #pragma unroll
                 for (int q = 0; q < 3; q++) {
@@ -693,7 +693,7 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
 
 template <int NT>
 __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
-                                            const int* tok, int pair0, uint64_t* stamp = nullptr) {
+                                            const int* tok, int pair0, uint64_t& stamp) {
     if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
     else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
     else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
@@ -703,9 +703,18 @@ __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, i
 
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
 // slot and n_shared + rank for a routed one.
+// The fused kernel's combiner of a tile (the last slot's down unit) folds the combine into its own unit when every
+// (term, token, row) word of the tile fits kCombW words per thread: it loads the other units' outputs right after
+// its stream, before its own stores, and takes its own terms from shared memory, so no store round trip sits on the
+// kernel's last path.
+constexpr int kCombW = 3;
+__device__ __forceinline__ bool combine_in_unit(const ExpertArgs& a) {
+    return a.T * 64 * (a.d.n_shared + a.d.k) <= kCombW * kThreads;
+}
+
 template <int N>
 __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank, uint64_t* stamp) {
+                          const int* rank, uint64_t& stamp, bool comb, const lds_RouteTab* crt) {
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = F / 8;
@@ -742,7 +751,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
             if (aneed(m)) dst[i0 + m * (int)blockDim.x + (int)threadIdx.x] = (unsigned)w[m];
     }
     __syncthreads();
-    if (stamp && threadIdx.x == 0) *stamp = __builtin_amdgcn_s_memrealtime();
+    stamp = __builtin_amdgcn_s_memrealtime();
     int xoff[N];
 #pragma unroll
     for (int j = 0; j < N; j++) xoff[j] = j < ntok ? j * nc : 0;
@@ -751,19 +760,78 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     for (int j = 0; j < N; j++) acc[j] = 0.f;
     if (!q8) tb.run(s.as, xoff, acc);
     else tq.run(s.as, xoff, acc);
+    const int S = a.d.n_shared, k = a.d.k, kq = S + k, ne = a.T * 64;
+    // combiner (comb; crt is its routing table): word w = q * ne + t * 64 + row of the tile; this unit's own terms
+    // come from its reduction.  (An LDS pointer can sit at address 0: never test one against null.)
+    auto own = [&](int q, int t) {
+        bool o = false;
+#pragma unroll
+        for (int j = 0; j < N; j++) o = o || (j < ntok && tok[j] == t && (e < 0 ? sl : S + rank[j]) == q);
+        return o;
+    };
+    auto cneed = [&](int m) {
+        const int w = (int)threadIdx.x + m * (int)blockDim.x;
+        if (w >= kq * ne) return false;
+        const int q = w / ne, t = (w % ne) / 64;
+        const bool live = q < S ? q < a.n_shared : (q - S < a.keep && crt->id[t * k + q - S] >= 0);
+        return live && !own(q, t);
+    };
+    auto cptr = [&](int m) {
+        const int w = (int)threadIdx.x + m * (int)blockDim.x;
+        const int q = w / ne, i = w % ne;
+        return a.ypart + ((size_t)(i / 64) * kq + q) * H + ht * 64 + i % 64;
+    };
+    uint64_t cw[kCombW];
+    if (comb) {
+#pragma unroll
+        for (int m = 0; m < kCombW; m++)
+            if (cneed(m)) cw[m] = ld_sync(cptr(m));
+    }
     reduce_waves<N>(s.red, acc, N);
-    if (wave == 0) {
+    const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + 2 * F + ht * 64 + lane] : 1.f;
+    if (wave == 0 && !comb) {  // a combiner's own outputs are read by no other unit
         const int h = ht * 64 + lane;
-        const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + 2 * F + h] : 1.f;
-        const int kq = a.d.n_shared + a.d.k;
 #pragma unroll
         for (int j = 0; j < N; j++) {
             if (j < ntok) {
-                const int q = e < 0 ? sl : a.d.n_shared + rank[j];
+                const int q = e < 0 ? sl : S + rank[j];
                 float y = s.red[j * 64 + lane];
                 if (q8) y = y * scale;
                 st_tag(&a.ypart[((size_t)tok[j] * kq + q) * H + h], a.epoch, __float_as_uint(y));
             }
+        }
+    }
+    if (comb) {
+        lds_float* cv = (lds_float*)s.as;  // [kq][T][64] terms of the tile
+        settle(cw, cptr, cneed, a.epoch, a.err);
+#pragma unroll
+        for (int m = 0; m < kCombW; m++) {
+            const int w = (int)threadIdx.x + m * (int)blockDim.x;
+            if (cneed(m)) cv[w] = __uint_as_float((unsigned)cw[m]);
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < N; j++) {
+                if (j < ntok) {
+                    float y = s.red[j * 64 + lane];
+                    if (q8) y = y * scale;
+                    cv[(e < 0 ? sl : S + rank[j]) * ne + tok[j] * 64 + lane] = y;
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < ne; i += blockDim.x) {  // fixed order: shared terms, then ranks
+            const int t = i / 64;
+            const size_t o = (size_t)t * H + ht * 64 + i % 64;
+            float acc2 = a.accumulate ? a.out[o] : 0.f;
+            for (int q = 0; q < kq; q++) {
+                if (q < S) {
+                    if (q < a.n_shared) acc2 = acc2 + cv[q * ne + i];
+                } else if (q - S < a.keep && crt->id[t * k + q - S] >= 0) {
+                    acc2 = fmaf(crt->gate[t * k + q - S], cv[q * ne + i], acc2);
+                }
+            }
+            a.out[o] = acc2;
         }
     }
     __syncthreads();  // s.as / s.red are reused by the next unit
@@ -771,12 +839,12 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
 
 template <int NT>
 __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank, uint64_t* stamp = nullptr) {
-    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, stamp);
-    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
-    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
-    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, stamp);
-    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, stamp);
+                          const int* rank, uint64_t& stamp, bool comb = false, const lds_RouteTab* crt = nullptr) {
+    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
+    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
+    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
+    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
+    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
 }
 
 // Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
@@ -884,7 +952,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     SlotView<NT> v;
     v.load(a.slots, sl);
     stage_x(s, a.x, a.T, a.d.H);
-    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0);
+    uint64_t stamp = 0;
+    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, stamp);
 }
 
 // Routing table of the combine, from the published slot table.
@@ -907,7 +976,8 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
     if (sl < a.slots->nslot && (sl >= a.d.n_shared || sl < a.n_shared)) {  // else unused / left out
         SlotView<NT> v;
         v.load(a.slots, sl);
-        down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank);
+        uint64_t stamp = 0;
+        down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, stamp);
     }
     if (sl == a.maxs - 1) {  // the last slot's unit of each tile combines it
         load_combine_table(rt, a.slots, a.T, a.d.k);
@@ -1004,7 +1074,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         }
         const UnitRef ur = decode_unit(u, f.nR, S, maxs, g, nht, f.lag);
         uint64_t t_ready = 0, t_aux = 0;
-        uint64_t* aux = f.trace ? &t_aux : nullptr;
+        uint64_t& aux = t_aux;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
             router_unit<NT>(s, a.L.wr, ur.idx * kWaves, a.d.E, H, a.T, f.logits, nullptr, a.epoch,
@@ -1036,6 +1106,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             }
         } else {
             const int sl = ur.sl, ht = ur.idx;
+            bool combined = false;
             if (sl < S) {  // shared slot: all tokens in order, no routing dependency
                 if (sl < a.n_shared) {
                     int tok[NT], rank[NT];
@@ -1051,11 +1122,13 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                 if (sl < rt->nslot) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
-                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, aux);
+                    const bool fold = sl == maxs - 1 && combine_in_unit(a);
+                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, aux, fold, rt);
+                    combined = fold;
                 }
             }
             if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
-            if (sl == maxs - 1) {  // the last slot's unit of each tile combines it
+            if (sl == maxs - 1 && !combined) {  // the last slot's unit of each tile combines it
                 ensure_routed();
                 combine_tile(a, rt, ht);
             }
