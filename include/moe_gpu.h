@@ -142,9 +142,10 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
- * {start, inputs ready (0 if the unit has none), end, workgroup, aux, 0} in the 100 MHz s_memrealtime clock (aux: when a
- * gate|up tile's finishing part has its sibling parts' sums, or a down unit its act rows; else 0); read_trace copies
- * the last launch's records (6 uint64 per unit, in the fused kernel's unit order). */
+ * {start, inputs ready, end, workgroup, aux, aux2} in the 100 MHz s_memrealtime clock.  Inputs ready: a routed gate|up
+ * part's routing known, a combining down unit's other terms in, else 0; aux: a gate|up tile's finishing part has its
+ * sibling parts' sums, a down unit its act rows, else 0; aux2: a down unit's weight stream done, else 0.  read_trace
+ * copies the last launch's records (6 uint64 per unit, in the fused kernel's unit order). */
 int moe_gpu_trace_units(moe_gpu* ctx, int on);
 int moe_gpu_read_trace(moe_gpu* ctx, uint64_t* buf, int max_units, int* units);
 /* Per-kernel profiling: with on != 0 every kernel launched by the compute calls is bracketed by a hipEvent pair on the

@@ -93,7 +93,9 @@ struct Sync {
 };
 
 // Unit trace record (fused kernel, optional): start, inputs ready, end (100 MHz s_memrealtime ticks), workgroup,
-// aux (gate|up finishing part: sibling partials in; down unit: act rows staged; else 0), reserved.
+// aux, aux2.  Inputs ready: routed gate|up part: routing known; combining down unit: the other terms in; else 0.
+// aux: gate|up finishing part: sibling partials in; down unit: act rows staged; else 0.  aux2: down unit: weight
+// stream done; else 0.
 constexpr int kTraceFields = 6;
 
 struct FusedArgs {

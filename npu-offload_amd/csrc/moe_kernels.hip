@@ -166,13 +166,19 @@ __device__ __forceinline__ void dot_chunk_q8(const u32x4 w, const lds_u32x4* xs,
 // loads alternate (load B, consume A, reload A, consume B), so D to 2D loads are always in flight and a reload only
 // ever targets a bank that has been consumed; the steady-state loop has no branches.  begin() issues the first bank,
 // so a caller can start the stream before it waits for the activations (run() consumes them).
-#ifndef MOE_STREAM_DEPTH
-#define MOE_STREAM_DEPTH 8  // loads per register bank (1 KB each per wavefront)
+// Loads per register bank (1 KB each per wavefront) of the gate|up and down streams.  On the Solar layer 8 measured
+// best for both: depths 4 to 20 were all slower, and so was interleaving the 4 wavefronts chunk by chunk (each
+// wavefront streams a contiguous quarter of its part).
+#ifndef MOE_GU_DEPTH
+#define MOE_GU_DEPTH 8
 #endif
-template <int N, bool Q8>
+#ifndef MOE_DN_DEPTH
+#define MOE_DN_DEPTH 8
+#endif
+template <int N, bool Q8, int DEPTH>
 struct TileStream {
     // wide token counts hold N activation chunks per weight chunk in registers: at most 4 loads per bank
-    static constexpr int D = N >= 8 ? (MOE_STREAM_DEPTH < 4 ? MOE_STREAM_DEPTH : 4) : MOE_STREAM_DEPTH;
+    static constexpr int D = N >= 8 ? (DEPTH < 4 ? DEPTH : 4) : DEPTH;
     const u32x4* p;
     int c0, c1;
     u32x4 A[D];
@@ -210,10 +216,18 @@ struct TileStream {
         } else if (nb - b == 1) {
             consume(A, c0 + b * D, xs, xoff, acc);
         }
-        for (int c = c0 + nb * D; c < c1; c++) {  // fewer than D leftover chunks
-            const u32x4 w = ld_stream(p + (size_t)c * 64);
-            if (Q8) dot_chunk_q8<N>(w, xs, xoff, c, acc);
-            else dot_chunk_bf16<N>(w, xs, xoff, c, acc);
+        const int cl = c0 + nb * D;  // fewer than D leftover chunks: all their loads issued, then consumed in order
+        if (cl < c1) {
+#pragma unroll
+            for (int u = 0; u < D; u++)
+                if (cl + u < c1) B[u] = ld_stream(p + (size_t)(cl + u) * 64);
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                if (cl + u < c1) {
+                    if (Q8) dot_chunk_q8<N>(B[u], xs, xoff, cl + u, acc);
+                    else dot_chunk_bf16<N>(B[u], xs, xoff, cl + u, acc);
+                }
+            }
         }
     }
 };
@@ -221,7 +235,7 @@ struct TileStream {
 template <int N, bool Q8>
 __device__ __forceinline__ void tile_stream(const u32x4* __restrict__ tile, int c0, int c1, const lds_u32x4* xs,
                                             const int* xoff, float* acc) {
-    TileStream<N, Q8> ts;
+    TileStream<N, Q8, MOE_GU_DEPTH> ts;
     ts.begin(tile, c0, c1);
     ts.run(xs, xoff, acc);
 }
@@ -708,20 +722,27 @@ __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, i
 // its stream, before its own stores, and takes its own terms from shared memory, so no store round trip sits on the
 // kernel's last path.
 constexpr int kCombW = 3;
+// Trace stamps of a down unit (taken when `on`): act rows staged, weight stream done, a combining unit's other
+// terms in.
+struct DownStamps {
+    bool on = false;
+    uint64_t aux = 0, run = 0, ready = 0;
+};
 __device__ __forceinline__ bool combine_in_unit(const ExpertArgs& a) {
     return a.T * 64 * (a.d.n_shared + a.d.k) <= kCombW * kThreads;
 }
 
 template <int N>
 __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank, uint64_t& stamp, bool comb, const lds_RouteTab* crt) {
+                          const int* rank, DownStamps& st, bool comb, const lds_RouteTab* crt) {
     const int H = a.d.H, F = a.d.F;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = F / 8;
-    // the weight stream starts first: its first bank is in flight while the act rows are polled
+    // the weight stream starts first: its first bank is in flight while the act rows are polled (a second bank
+    // here, or the act loads ahead of the bank, measured slower)
     const bool q8 = a.int8 && e >= 0;
-    TileStream<N, false> tb;
-    TileStream<N, true> tq;
+    TileStream<N, false, MOE_DN_DEPTH> tb;
+    TileStream<N, true, MOE_DN_DEPTH> tq;
     if (!q8) {
         const uint16_t* base =
             e >= 0 ? a.L.dn + (size_t)e * a.d.dn_stride() : a.L.sdn + (size_t)(-1 - e) * a.d.dn_stride();
@@ -751,7 +772,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
             if (aneed(m)) dst[i0 + m * (int)blockDim.x + (int)threadIdx.x] = (unsigned)w[m];
     }
     __syncthreads();
-    stamp = __builtin_amdgcn_s_memrealtime();
+    if (st.on) st.aux = __builtin_amdgcn_s_memrealtime();
     int xoff[N];
 #pragma unroll
     for (int j = 0; j < N; j++) xoff[j] = j < ntok ? j * nc : 0;
@@ -760,6 +781,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     for (int j = 0; j < N; j++) acc[j] = 0.f;
     if (!q8) tb.run(s.as, xoff, acc);
     else tq.run(s.as, xoff, acc);
+    if (st.on) st.run = __builtin_amdgcn_s_memrealtime();
     const int S = a.d.n_shared, k = a.d.k, kq = S + k, ne = a.T * 64;
     // combiner (comb; crt is its routing table): word w = q * ne + t * 64 + row of the tile; this unit's own terms
     // come from its reduction.  (An LDS pointer can sit at address 0: never test one against null.)
@@ -804,6 +826,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     if (comb) {
         lds_float* cv = (lds_float*)s.as;  // [kq][T][64] terms of the tile
         settle(cw, cptr, cneed, a.epoch, a.err);
+        if (st.on) st.ready = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
         for (int m = 0; m < kCombW; m++) {
             const int w = (int)threadIdx.x + m * (int)blockDim.x;
@@ -839,12 +862,12 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
 
 template <int NT>
 __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
-                          const int* rank, uint64_t& stamp, bool comb = false, const lds_RouteTab* crt = nullptr) {
-    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
-    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
-    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
-    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
-    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, stamp, comb, crt);
+                          const int* rank, DownStamps& st, bool comb = false, const lds_RouteTab* crt = nullptr) {
+    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
 }
 
 // Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
@@ -976,7 +999,7 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
     if (sl < a.slots->nslot && (sl >= a.d.n_shared || sl < a.n_shared)) {  // else unused / left out
         SlotView<NT> v;
         v.load(a.slots, sl);
-        uint64_t stamp = 0;
+        DownStamps stamp;
         down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, stamp);
     }
     if (sl == a.maxs - 1) {  // the last slot's unit of each tile combines it
@@ -1062,18 +1085,18 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         }
     };
     uint64_t t_start = 0;
+    int next = 0;  // thread 0: the unit after the current one
     // Units b and grid + b are this workgroup's first two (no queue traffic while every workgroup starts at once);
     // from the second unit on, the index after the current one is fetched from the queue while the current one runs.
     const int grid = (int)gridDim.x;
     for (int u = blockIdx.x, round = 0; u < uEnd; round++) {
-        int next = 0;
         if (threadIdx.x == 0) {
             if (round == 0) next = grid + (int)blockIdx.x;
             else next = 2 * grid + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
         }
         const UnitRef ur = decode_unit(u, f.nR, S, maxs, g, nht, f.lag);
-        uint64_t t_ready = 0, t_aux = 0;
+        uint64_t t_ready = 0, t_aux = 0, t_aux2 = 0;
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
@@ -1107,6 +1130,8 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         } else {
             const int sl = ur.sl, ht = ur.idx;
             bool combined = false;
+            DownStamps ds;
+            ds.on = f.trace != nullptr;
             if (sl < S) {  // shared slot: all tokens in order, no routing dependency
                 if (sl < a.n_shared) {
                     int tok[NT], rank[NT];
@@ -1115,7 +1140,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                         tok[j] = j;
                         rank[j] = -1;
                     }
-                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank, aux);
+                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank, ds);
                 }
             } else {
                 ensure_routed();
@@ -1123,11 +1148,13 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
                     const bool fold = sl == maxs - 1 && combine_in_unit(a);
-                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, aux, fold, rt);
+                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, ds, fold, rt);
                     combined = fold;
                 }
             }
-            if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
+            t_aux = ds.aux;
+            t_aux2 = ds.run;
+            t_ready = ds.ready;
             if (sl == maxs - 1 && !combined) {  // the last slot's unit of each tile combines it
                 ensure_routed();
                 combine_tile(a, rt, ht);
@@ -1140,7 +1167,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             tr[2] = __builtin_amdgcn_s_memrealtime();
             tr[3] = blockIdx.x;
             tr[4] = t_aux;
-            tr[5] = 0;
+            tr[5] = t_aux2;
         }
         __syncthreads();  // the whole workgroup is done with unit u before s_unit changes
         if (threadIdx.x == 0) s_unit = next;
