@@ -210,12 +210,14 @@ def main():
         tier.profile_kernels(False)
         kernels = {n: {"avg_us": round(ms / max(c, 1) * 1e3, 2), "launches": c} for n, (ms, c) in prof.items() if c}
         if prof.get("fused_layer_kernel", (0, 0))[1]:
-            # one fused kernel streams everything the layer reads: router, routed experts, shared expert
-            k_name, (k_ms, k_n) = "fused_layer_kernel", prof["fused_layer_kernel"]
+            # one fused kernel streams everything the layer reads: router, routed experts, shared expert.  It is the
+            # only kernel of a step, so its average launch duration is the timed region's event time over the K
+            # back-to-back launches on its stream (the per-kernel event pairs of this pass add their own overhead).
+            k_name, k_ms, k_n = "fused_layer_kernel", ev_ms, K
             k_bytes = avg_bytes
         else:
             # unfused: gate|up streams 2/3 of every expert's bytes and dominates
-            k_name, (k_ms, k_n) = "gateup_kernel", prof["gateup_kernel"]
+            (k_ms, k_n), k_name = prof["gateup_kernel"], "gateup_kernel"
             per_expert_gu = 2 * w.F * w.H * (1 if w.int8 else 2)
             k_bytes = float(np.mean([u * per_expert_gu + w.n_shared * 2 * w.F * w.H * 2 for u in distinct]))
         k_avg_s = k_ms / k_n * 1e-3

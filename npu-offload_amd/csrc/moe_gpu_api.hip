@@ -70,7 +70,8 @@ struct moe_gpu {
     bool fused = true;     // one persistent kernel per layer call (MOE_GPU_OPT_FUSED)
     int wg_per_cu = 1;     // fused grid: workgroups per CU, 0 = as many as fit (MOE_GPU_OPT_WG_PER_CU)
     int last_grid = 0;
-    int ksplit = 0;        // K parts per gate|up tile, 0 = automatic (MOE_GPU_OPT_KSPLIT)
+    int ksplit = 0;        // K parts per routed gate|up tile, 0 = automatic (MOE_GPU_OPT_KSPLIT)
+    int ksplit_shared = 0; // K parts per shared gate|up tile, 0 = automatic (MOE_GPU_OPT_KSPLIT_SHARED)
     int lag = 0;           // fused queue lag of down blocks, 0 = automatic (MOE_GPU_OPT_LAG)
     int shared_waits = 0;  // MOE_GPU_OPT_SHARED_WAITS
     uint64_t* d_gpart = nullptr;    // tagged split gate|up partial sums
@@ -287,12 +288,17 @@ int next_epoch(moe_gpu* c, unsigned* ep) {
 
 // K parts per gate|up tile: the option, else about 256 KiB of weights per part (64 rows x H / kp), the size that
 // measured best for the fused schedule at H = 4096 (smaller parts add per-unit latency, larger ones a longer tail).
-static int kparts(const moe_gpu* c, bool int8) {
-    if (c->ksplit > 0) return c->ksplit;
-    const size_t tile = (size_t)64 * c->d.H * (int8 ? 1 : 2);
+static int kparts_for(size_t tile) {
     int kp = 1;
-    while (kp < 4 && tile / (kp * 2) >= ((size_t)256 << 10)) kp *= 2;
+    while (kp < moe::kMaxKp && tile / (kp * 2) >= ((size_t)256 << 10)) kp *= 2;
     return kp;
+}
+static int kparts(const moe_gpu* c, bool int8) {
+    return c->ksplit > 0 ? c->ksplit : kparts_for((size_t)64 * c->d.H * (int8 ? 1 : 2));
+}
+// The shared experts stay bf16 in an int8 call: their parts are sized by their own bytes.
+static int kparts_shared(const moe_gpu* c) {
+    return c->ksplit_shared > 0 ? c->ksplit_shared : kparts_for((size_t)64 * c->d.H * 2);
 }
 
 // The expert pipeline of one call.  do_topk: route on the device from the layer's router (ids/gates are outputs);
@@ -310,6 +316,7 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
     a.kp = kparts(c, a.int8 != 0);
+    a.kps = kparts_shared(c);
     a.gpart = c->d_gpart;
     if ((rc = next_epoch(c, &a.epoch))) return rc;
     a.err = &c->d_sync->err;
@@ -324,7 +331,7 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
         f.lag = c->lag > 0 ? c->lag : 8;
         f.phase = (int)(c->fused_launches++ & 1u);
         f.shared_waits = c->shared_waits;
-        c->trace_units = moe::fused_units(f.nR, a.maxs, c->d.F, c->d.H, a.kp);
+        c->trace_units = moe::fused_units(f.nR, a.maxs, c->d.n_shared, c->d.F, c->d.H, a.kp, a.kps);
         LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->stream, &c->last_grid));
         return MOE_GPU_OK;
     }
@@ -426,7 +433,7 @@ int moe_gpu_create(int device, int H, int F, int E, int topk, int n_shared, int 
     if ((rc = dev_alloc(c, (void**)&c->d_act, c->act_bytes, "act"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_ypart, c->ypart_bytes, "ypart"))) return bail(rc);
     // split gate|up partials: at most max_tokens * (n_shared + topk) (slot, token) pairs, 4 parts per tile
-    c->gpart_bytes = (size_t)max_tokens * kq * (F / 32) * 4 * 64 * 8;
+    c->gpart_bytes = (size_t)max_tokens * kq * (F / 32) * moe::kMaxKp * 64 * 8;
     if ((rc = dev_alloc(c, (void**)&c->d_gpart, c->gpart_bytes, "gate|up partials"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage, (size_t)3 * F * H * 2, "staging"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage_q8, (size_t)3 * F * H, "int8 staging"))) return bail(rc);
@@ -767,6 +774,11 @@ int moe_gpu_set_option(moe_gpu* c, int opt, int value) {
                 return fail(c, MOE_GPU_EINVAL, "K split %d not in {0, 1, 2, 4}", value);
             c->ksplit = value;
             return MOE_GPU_OK;
+        case MOE_GPU_OPT_KSPLIT_SHARED:
+            if (value != 0 && value != 1 && value != 2 && value != 4)
+                return fail(c, MOE_GPU_EINVAL, "shared K split %d not in {0, 1, 2, 4}", value);
+            c->ksplit_shared = value;
+            return MOE_GPU_OK;
         case MOE_GPU_OPT_LAG:
             if (value < 0) return fail(c, MOE_GPU_EINVAL, "lag %d < 0", value);
             c->lag = value;
@@ -781,7 +793,8 @@ int moe_gpu_trace_units(moe_gpu* c, int on) {
     if (rc) return rc;
     if (on && !c->d_trace) {
         const size_t units = (size_t)moe::fused_units((c->d.E + moe::kWaves - 1) / moe::kWaves,
-                                                      c->d.n_shared + c->d.max_t * c->d.k, c->d.F, c->d.H, 4);
+                                                      c->d.n_shared + c->d.max_t * c->d.k, c->d.n_shared, c->d.F,
+                                                      c->d.H, moe::kMaxKp, moe::kMaxKp);
         const size_t bytes = units * moe::kTraceFields * sizeof(uint64_t);
         if ((rc = dev_alloc(c, (void**)&c->d_trace, bytes, "unit trace"))) return rc;
         HIPCHK(c, hipMemset(c->d_trace, 0, bytes));
@@ -816,6 +829,7 @@ int moe_gpu_get_option(moe_gpu* c, int opt, int* value) {
         case MOE_GPU_OPT_KSPLIT: *value = c->ksplit; return MOE_GPU_OK;
         case MOE_GPU_OPT_LAG: *value = c->lag; return MOE_GPU_OK;
         case MOE_GPU_OPT_SHARED_WAITS: *value = c->shared_waits; return MOE_GPU_OK;
+        case MOE_GPU_OPT_KSPLIT_SHARED: *value = c->ksplit_shared; return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
 }

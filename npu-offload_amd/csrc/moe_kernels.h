@@ -61,6 +61,7 @@ __host__ __device__ inline int gu_row_f(int tile, int i) { return 32 * tile + 8 
 __host__ __device__ inline int gu_row_up(int i) { return (i >> 3) & 1; }
 
 constexpr int kMaxHTiles = 256;  // H <= 16384 (64-row down tiles)
+constexpr int kMaxKp = 4;        // K parts of a gate|up tile
 
 // Everything one expert pipeline call needs (device pointers).
 struct ExpertArgs {
@@ -76,8 +77,9 @@ struct ExpertArgs {
     // cross-workgroup intermediates, tagged words (epoch << 32) | payload
     uint64_t* act;                            // [maxs][max_t][F/2] pairs of bf16 SiLU(g)*u
     uint64_t* ypart;                          // [T][n_shared + k][H] fp32 down outputs
-    uint64_t* gpart;                          // [pairs][F/32][kp][64] fp32 partial sums of split gate|up tiles
-    int kp;                                   // K parts of a gate|up tile (1, 2 or 4): one unit each
+    uint64_t* gpart;                          // [pairs][F/32][kMaxKp][64] fp32 partial sums of split gate|up tiles
+    int kp;                                   // K parts of a routed slot's gate|up tile (1, 2 or 4): one unit each
+    int kps;                                  // K parts of a shared slot's gate|up tile (1, 2 or 4)
     unsigned epoch;                           // this call's tag (never 0)
     unsigned* err;                            // set when a bounded wait gave up (sticky until the host clears it)
 };
@@ -110,9 +112,14 @@ struct FusedArgs {
     int shared_waits;  // 1: shared gate|up parts start only once the routing is known
 };
 
-// Fused-kernel unit count: router units, the route publisher, then every slot's gate|up and down units.
-__host__ __device__ inline int fused_units(int nR, int maxs, int F, int H, int kp) {
-    return nR + 1 + maxs * (F / 32) * kp + maxs * (H / 64);
+// Fused-kernel unit count: router units, the route publisher, then every slot's gate|up and down units (S shared
+// slots of kps parts per gate|up tile, maxs - S routed slots of kp parts).
+__host__ __device__ inline int fused_units(int nR, int maxs, int S, int F, int H, int kp, int kps) {
+    return nR + 1 + (S * kps + (maxs - S) * kp) * (F / 32) + maxs * (H / 64);
+}
+// Gate|up units of the unfused kernel: one per (slot, tile, K part), shared slots first.
+__host__ __device__ inline int gateup_units(int maxs, int S, int F, int kp, int kps) {
+    return (S * kps + (maxs - S) * kp) * (F / 32);
 }
 
 size_t lds_bytes(int T, int NT, int H, int F, int E);

@@ -634,14 +634,15 @@ __device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int
 
 // --------------------------------------------------------------------------------------------------------------------
 // Unit: gate|up tile part.  Slot s, 32 f values = one 64-row tile (32 gate rows + their 32 up rows), K part kpi of
-// a.kp (chunks [kpi, kpi + 1) * H/8/kp), the 4 wavefronts splitting the part; act[s][j][f] = bf16(silu(g) * u) for
+// kp (a.kps for a shared slot, a.kp for a routed one; chunks [kpi, kpi + 1) * H/8/kp), the 4 wavefronts splitting the
+// part; act[s][j][f] = bf16(silu(g) * u) for
 // the slot's tokens.  Sums: wavefronts in order within a part, then parts in order.  Parts below kp - 1 publish their
 // partial sums to gpart; part kp - 1 (the tile's last unit in queue order) reads them back, finishes the tile and
 // publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
 template <int N>
 __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
                                             const int* tok, int pair0, uint64_t& stamp) {
-    const int H = a.d.H, F = a.d.F, kp = a.kp, ntile = F / 32;
+    const int H = a.d.H, F = a.d.F, kp = e < 0 ? a.kps : a.kp, ntile = F / 32;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int nc = H / 8;
     int xoff[N];
@@ -665,19 +666,20 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
     }
     reduce_waves<N>(s.red, acc, N);
     if (wave == 0) {
-        uint64_t* gp0 = a.gpart + (((size_t)pair0 * ntile + tile) * kp) * 64 + lane;  // + (j * ntile * kp + q) * 64
+        uint64_t* gp0 = a.gpart + (((size_t)pair0 * ntile + tile) * kMaxKp) * 64 + lane;  // + (j*ntile*kMaxKp + q)*64
         if (kpi < kp - 1) {
 #pragma unroll
             for (int j = 0; j < N; j++)
-                if (j < ntok) st_tag(gp0 + ((size_t)j * ntile * kp + kpi) * 64, a.epoch, __float_as_uint(s.red[j * 64 + lane]));
+                if (j < ntok)
+                    st_tag(gp0 + ((size_t)j * ntile * kMaxKp + kpi) * 64, a.epoch, __float_as_uint(s.red[j * 64 + lane]));
         } else {
             const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + tile * 64 + lane] : 1.f;
-            uint64_t w[N][3];  // the other parts' partials: all loads issued before any use
-            auto gptr = [&](int j, int q) { return gp0 + ((size_t)(j < ntok ? j : 0) * ntile * kp + q) * 64; };
+            uint64_t w[N][kMaxKp - 1];  // the other parts' partials: all loads issued before any use
+            auto gptr = [&](int j, int q) { return gp0 + ((size_t)(j < ntok ? j : 0) * ntile * kMaxKp + q) * 64; };
 #pragma unroll
             for (int j = 0; j < N; j++)
 #pragma unroll
-                for (int q = 0; q < 3; q++)
+                for (int q = 0; q < kMaxKp - 1; q++)
                     if (q < kp - 1) w[j][q] = ld_sync(gptr(j, q));
 #pragma unroll
             for (int j = 0; j < N; j++) {
@@ -685,7 +687,7 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
                 if (j == 0) stamp = __builtin_amdgcn_s_memrealtime();
                 float v = 0.f;
 #pragma unroll
-                for (int q = 0; q < 3; q++) {
+                for (int q = 0; q < kMaxKp - 1; q++) {
                     if (q < kp - 1) {
                         const float pv = __uint_as_float((unsigned)w[j][q]);
                         v = q == 0 ? pv : v + pv;
@@ -969,8 +971,10 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     if (blockIdx.x == 0 && threadIdx.x < 2) st_sync(&sy->next_unit[threadIdx.x * kSyncPad], 0u);  // fused queue heads
-    const int ntile = a.d.F / 32, g = ntile * a.kp;
-    const int sl = blockIdx.x / g, tile = (blockIdx.x % g) / a.kp, kpi = blockIdx.x % a.kp;
+    const int ntile = a.d.F / 32, S = a.d.n_shared, gs = ntile * a.kps, g = ntile * a.kp;
+    const int b = (int)blockIdx.x, shared = b < S * gs;  // shared slots' parts first
+    const int kp = shared ? a.kps : a.kp, ub = shared ? b : b - S * gs;
+    const int sl = shared ? b / gs : S + ub / g, tile = (ub % (shared ? gs : g)) / kp, kpi = ub % kp;
     if (sl >= a.slots->nslot || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
     SlotView<NT> v;
     v.load(a.slots, sl);
@@ -1026,13 +1030,13 @@ struct UnitRef {
     int kind;  // 0 router, 1 publisher, 2 gate|up part, 3 down tile
     int sl, idx;
 };
-__device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int g, int nht, int lag) {
+__device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int gs, int g, int nht, int lag) {
     if (u < uR) return {0, 0, u};
     u -= uR;
     if (u < 1) return {1, 0, 0};
     u -= 1;
-    if (u < S * g) return {2, u / g, u % g};  // shared slots' gate|up parts
-    u -= S * g;
+    if (u < S * gs) return {2, u / gs, u % gs};  // shared slots' gate|up parts (gs per slot)
+    u -= S * gs;
     if (u < S * nht) return {3, u / nht, u % nht};  // shared slots' downs (no routing needed)
     u -= S * nht;
     const int Mr = M - S;               // routed slots S .. M - 1, numbered r = slot - S below
@@ -1058,9 +1062,9 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     Sync* sy = f.sync;
     const int H = a.d.H, F = a.d.F, S = a.d.n_shared;
-    const int ntile = F / 32, nht = H / 64, g = ntile * a.kp;
+    const int ntile = F / 32, nht = H / 64, g = ntile * a.kp, gs = ntile * a.kps;
     const int maxs = a.maxs;
-    const int uEnd = fused_units(f.nR, maxs, F, H, a.kp);
+    const int uEnd = fused_units(f.nR, maxs, S, F, H, a.kp, a.kps);
     const int ph = f.phase & 1;
     unsigned* queue = &sy->next_unit[ph * kSyncPad];
     if (threadIdx.x == 0) {
@@ -1095,7 +1099,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             else next = 2 * grid + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
         }
-        const UnitRef ur = decode_unit(u, f.nR, S, maxs, g, nht, f.lag);
+        const UnitRef ur = decode_unit(u, f.nR, S, maxs, gs, g, nht, f.lag);
         uint64_t t_ready = 0, t_aux = 0, t_aux2 = 0;
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
@@ -1108,7 +1112,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             if (f.trace) t_ready = __builtin_amdgcn_s_memrealtime();
             route_publish(rt, a.T, a.d.k, a.keep, S, f.do_topk, a.ids, a.gates, a.slots);
         } else if (ur.kind == 2) {
-            const int sl = ur.sl, tile = ur.idx / a.kp, kpi = ur.idx % a.kp;
+            const int sl = ur.sl, kp = sl < S ? a.kps : a.kp, tile = ur.idx / kp, kpi = ur.idx % kp;
             ensure_staged();  // x first: its load overlaps the wait for the routing
             if (sl < S) {  // shared slot: all tokens in order, no routing dependency
                 if (f.shared_waits) ensure_routed();  // optional: keep the memory system quiet while routing
@@ -1371,7 +1375,7 @@ static hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&gateup_kernel<NT>), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gateup_kernel<NT>, dim3(maxs * (ea.d.F / 32) * ea.kp), dim3(256), lds, st, ea, sy);
+    hipLaunchKernelGGL(gateup_kernel<NT>, dim3(gateup_units(maxs, ea.d.n_shared, ea.d.F, ea.kp, ea.kps)), dim3(256), lds, st, ea, sy);
     return hipGetLastError();
 }
 
@@ -1424,7 +1428,7 @@ static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid
     int per_cu = c_per_cu, ncu = c_ncu;
     if (wg_per_cu > 0 && wg_per_cu < per_cu) per_cu = wg_per_cu;
     if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const int units = fused_units(f.nR, f.e.maxs, f.e.d.F, f.e.d.H, f.e.kp);
+    const int units = fused_units(f.nR, f.e.maxs, f.e.d.n_shared, f.e.d.F, f.e.d.H, f.e.kp, f.e.kps);
     int grid = ncu * per_cu;
     if (grid > units) grid = units;
     if (grid_out) *grid_out = grid;

@@ -37,7 +37,7 @@ SYMBOLS = (
     "moe_gpu_set_option", "moe_gpu_get_option", "moe_gpu_trace_units", "moe_gpu_read_trace",
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
 )
-OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS = 1, 2, 3, 4, 5, 6
+OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
 
 _lib = None
 

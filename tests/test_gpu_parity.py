@@ -429,9 +429,9 @@ def test_solar_queue_lag_does_not_change_bits(solar):
         tier.set_option(OPT_SHARED_WAITS, 0)
 
 
-@pytest.mark.parametrize("kp", [1, 2])
+@pytest.mark.parametrize("kp", [1, 4])
 def test_solar_ksplit_within_bars(solar, kp):
-    """Solar layer with other K splits than the automatic one (4 parts at H=4096): same ids, outputs within bars."""
+    """Solar layer with other K splits than the automatic one (2 parts at H=4096): same ids, outputs within bars."""
     from moe_gpu import OPT_KSPLIT
     tier, hl = solar
     x = random_x(1, SOLAR.H, np.random.default_rng(140 + kp))
@@ -444,6 +444,34 @@ def test_solar_ksplit_within_bars(solar, kp):
         tier.set_option(OPT_KSPLIT, 0)
     check_route(ids, gates, ref, SOLAR.k)
     assert_layer_close(out, ref["out"])
+
+
+@pytest.mark.parametrize("kp,kps", [(1, 2), (2, 1), (1, 4), (4, 1)])
+def test_solar_shared_ksplit_paths_and_bars(solar, kp, kps):
+    """The shared expert's gate|up K split set apart from the routed experts' (as an int8 call does: int8 routed
+    parts at kp 1, the bf16 shared expert at 2): fused and unfused give identical bits, bf16 and int8 outputs stay
+    within the bars of the oracle."""
+    from moe_gpu import OPT_FUSED, OPT_KSPLIT, OPT_KSPLIT_SHARED
+    tier, hl = solar
+    tier.quantize_layer(0)
+    x = random_x(2, SOLAR.H, np.random.default_rng(160 + 10 * kp + kps))
+    try:
+        tier.set_option(OPT_KSPLIT, kp)
+        tier.set_option(OPT_KSPLIT_SHARED, kps)
+        for flags, keep in ((0, 0), (INT8, 4)):
+            say(f"solar K split {kp} / shared {kps}, flags {flags}")
+            ref = oracle_layer(hl, x, keep=keep, int8=bool(flags))
+            tier.set_option(OPT_FUSED, 1)
+            of, idf, gf = tier.layer(0, x, keep=keep, flags=flags)
+            tier.set_option(OPT_FUSED, 0)
+            ou, idu, _ = tier.layer(0, x, keep=keep, flags=flags)
+            np.testing.assert_array_equal(idf, idu)
+            np.testing.assert_array_equal(of.view(np.uint32), ou.view(np.uint32))
+            assert_layer_close(of, ref["out"])
+    finally:
+        tier.set_option(OPT_FUSED, 1)
+        tier.set_option(OPT_KSPLIT, 0)
+        tier.set_option(OPT_KSPLIT_SHARED, 0)
 
 
 def test_fused_calls_interleaved_with_route_calls(solar):
