@@ -332,28 +332,33 @@ __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __rest
                 float wf[8];
                 unpack8(w[j], wf);
                 const int c = lane + 64 * (j0 + j);
+                // all NT columns, with no per-token branch (columns t >= T read token 0 and are discarded), so the
+                // shared-memory reads of a chunk are all in flight together
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    if (t < T) {
-                        float xf[8];
-                        unpack8(s.xs[t * nc + c], xf);
+                    float xf[8];
+                    unpack8(s.xs[(t < T ? t : 0) * nc + c], xf);
 #pragma unroll
-                        for (int i = 0; i < 8; i++) acc[t] = fmaf(wf[i], xf[i], acc[t]);
-                    }
+                    for (int i = 0; i < 8; i++) acc[t] = fmaf(wf[i], xf[i], acc[t]);
                 }
             }
         }
     }
     if (e >= E) return;
+    float v[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        if (t < T) {
-            float v = acc[t];
+    for (int t = 0; t < NT; t++) v[t] = acc[t];
 #pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            if (lane == 0) {
-                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(v));
-                if (logits_out) logits_out[(size_t)t * E + e] = v;
+    for (int m = 32; m >= 1; m >>= 1) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) v[t] = v[t] + __shfl_xor(v[t], m, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < T) {
+                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(v[t]));
+                if (logits_out) logits_out[(size_t)t * E + e] = v[t];
             }
         }
     }
@@ -950,7 +955,9 @@ __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T,
     const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
     const int e0 = blockIdx.x * kWaves;
     if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
+    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
     else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
+    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
     else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
 }
 
