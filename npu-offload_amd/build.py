@@ -16,7 +16,6 @@ LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libmoe_gpu.so")
 ARCH = os.environ.get("MOE_GPU_ARCH", "gfx950")
 
-SOURCES = ["moe_kernels.hip", "moe_gpu_api.hip"]
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_fma_f32 & co).
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -29,20 +28,49 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# The kernel source is compiled as parts in parallel (its token-bucket kernels dominate the compile time): part 0
+# holds everything else, part N only the kernels of token bucket N (MOE_PART in moe_kernels.hip).
+KERNEL_PARTS = [0, 1, 2, 4, 8, 16]
+
+
+def _jobs():
+    """(source, defines, object) for every object of the library."""
+    obj = os.path.join(PKG, "build")
+    jobs = [(os.path.join(CSRC, "moe_gpu_api.hip"), [], os.path.join(obj, "moe_gpu_api.o"))]
+    for part in KERNEL_PARTS:
+        jobs.append((os.path.join(CSRC, "moe_kernels.hip"), [f"-DMOE_PART={part}"],
+                     os.path.join(obj, f"moe_kernels_part{part}.o")))
+    return jobs
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
+    os.makedirs(os.path.join(PKG, "build"), exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    procs = []
+    for src, defs, obj in _jobs():
+        cmd = [hipcc(), f"--offload-arch={ARCH}", *HIPCC_FLAGS, *defs, *inc, "-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = False
+    for cmd, pr in procs:
+        out, _ = pr.communicate()
+        if pr.returncode != 0:
+            failed = True
+            sys.stderr.write(" ".join(cmd) + "\n" + out)
+        elif verbose and out.strip():
+            sys.stderr.write(out)
+    if failed:
+        raise RuntimeError("hipcc failed")
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", *HIPCC_FLAGS, "-shared",
-           "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-           *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for _, _, o in _jobs()], "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError(f"hipcc failed ({r.returncode})")
-    if verbose and r.stderr.strip():
-        sys.stderr.write(r.stderr)
+        raise RuntimeError(f"hipcc link failed ({r.returncode})")
     os.replace(tmp, LIB)
     return LIB
 

@@ -19,6 +19,18 @@
 
 namespace moe {
 
+// Build partitioning.  Compiled as one translation unit (MOE_PART undefined), or as parts compiled in parallel:
+// MOE_PART=0 holds everything except the token-bucket kernels, MOE_PART=N (1, 2, 4, 8, 16) only bucket N's kernels
+// and launchers (explicitly instantiated there, declared extern in part 0).
+#if !defined(MOE_PART)
+#define MOE_COMMON 1
+#elif MOE_PART == 0
+#define MOE_COMMON 1
+#define MOE_EXTERN_BUCKETS 1
+#else
+#define MOE_COMMON 0
+#endif
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 // LDS pointers carry their address space so that reads compile to ds_read (LGKM counter), never to flat loads that
@@ -277,9 +289,11 @@ __host__ __device__ inline size_t as_bytes(int NT, int F, int E) {
     return act > kRouteScratchBytes ? act : kRouteScratchBytes;
 }
 
+#if MOE_COMMON
 size_t lds_bytes(int T, int NT, int H, int F, int E) {
     return (size_t)T * (H / 8) * 16 + as_bytes(NT, F, E) + (size_t)4 * NT * 64 * 4;
 }
+#endif  // MOE_COMMON
 
 __device__ inline Lds lds_carve(unsigned char* base_generic, int T, int NT, int H, int F, int E) {
     LDS_AS unsigned char* base = (LDS_AS unsigned char*)base_generic;
@@ -948,6 +962,7 @@ struct SlotView {
 
 // ====================================================================================================================
 // Unfused path: one kernel per phase (stream order provides the dependencies; the tagged reads succeed at once).
+#if MOE_COMMON
 __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T, const uint16_t* __restrict__ x,
                                                      uint64_t* __restrict__ logits, float* __restrict__ logits_out,
                                                      unsigned epoch) {
@@ -972,6 +987,8 @@ __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, in
                 do_topk);
     route_publish(rt, T, d.k, keep, n_shared, do_topk, ids, gates, slots);
 }
+
+#endif  // MOE_COMMON
 
 template <int NT>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
@@ -1187,6 +1204,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     }
 }
 
+#if MOE_COMMON
 // --------------------------------------------------------------------------------------------------------------------
 // One-time layout kernels (one thread per 16-byte destination chunk).
 __global__ void relayout_gu_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, int H, int F,
@@ -1349,6 +1367,8 @@ __global__ void synth_fill_kernel(u32x4* __restrict__ dst, uint64_t nchunk, uint
 
 // ==================================================================================================================
 // launch helpers
+#endif  // MOE_COMMON
+
 static inline unsigned nblk(size_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
 static hipError_t set_lds(const void* fn, size_t lds) {
@@ -1358,6 +1378,7 @@ static hipError_t set_lds(const void* fn, size_t lds) {
 
 static int nt_bucket(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
+#if MOE_COMMON
 hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, uint64_t* logits,
                          float* logits_out, unsigned epoch, hipStream_t st) {
     const size_t lds = lds_bytes(T, 1, d.H, d.F, d.E);
@@ -1376,8 +1397,10 @@ hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep,
     return hipGetLastError();
 }
 
+#endif  // MOE_COMMON
+
 template <int NT>
-static hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
+hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     const int maxs = ea.maxs;
     const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&gateup_kernel<NT>), lds);
@@ -1387,7 +1410,7 @@ static hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
 }
 
 template <int NT>
-static hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
+hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
     const size_t lds = lds_bytes(0, NT, ea.d.H, ea.d.F, ea.d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&down_kernel<NT>), lds);
     if (e != hipSuccess) return e;
@@ -1395,6 +1418,25 @@ static hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int NT>
+hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out);
+#if defined(MOE_EXTERN_BUCKETS)
+#define MOE_BUCKET_DECL(N)                                                                         \
+    extern template hipError_t gateup_nt<N>(const ExpertArgs&, Sync*, hipStream_t);                \
+    extern template hipError_t down_nt<N>(const ExpertArgs&, hipStream_t);                         \
+    extern template hipError_t fused_nt<N>(FusedArgs, int, hipStream_t, int*);
+MOE_BUCKET_DECL(1)
+MOE_BUCKET_DECL(2)
+MOE_BUCKET_DECL(4)
+MOE_BUCKET_DECL(8)
+MOE_BUCKET_DECL(16)
+#endif
+#if defined(MOE_PART) && MOE_PART > 0
+template hipError_t gateup_nt<MOE_PART>(const ExpertArgs&, Sync*, hipStream_t);
+template hipError_t down_nt<MOE_PART>(const ExpertArgs&, hipStream_t);
+#endif
+
+#if MOE_COMMON
 hipError_t launch_gateup(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     switch (nt_bucket(ea.T)) {
         case 1: return gateup_nt<1>(ea, sy, st);
@@ -1415,8 +1457,10 @@ hipError_t launch_down(const ExpertArgs& ea, hipStream_t st) {
     }
 }
 
+#endif  // MOE_COMMON
+
 template <int NT>
-static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
+hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
     const void* fn = reinterpret_cast<const void*>(&fused_layer_kernel<NT>);
     const size_t lds = lds_bytes(f.e.T, NT, f.e.d.H, f.e.d.F, f.e.d.E);
     // occupancy per (device, LDS size), computed once: the launch itself stays a single host call
@@ -1443,6 +1487,11 @@ static hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid
     return hipGetLastError();
 }
 
+#if defined(MOE_PART) && MOE_PART > 0
+template hipError_t fused_nt<MOE_PART>(FusedArgs, int, hipStream_t, int*);
+#endif
+
+#if MOE_COMMON
 hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out) {
     switch (nt_bucket(f.e.T)) {
         case 1: return fused_nt<1>(f, wg_per_cu, st, grid_out);
@@ -1525,5 +1574,7 @@ hipError_t launch_zero(uint64_t* dst, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n);
     return hipGetLastError();
 }
+
+#endif  // MOE_COMMON
 
 }  // namespace moe
