@@ -218,7 +218,8 @@ class MoeGpu:
         self._chk(self.L.moe_gpu_trace_units(self.h, 1 if on else 0))
 
     def read_trace(self) -> np.ndarray:
-        """[units, 6] uint64: start, inputs ready, end (100 MHz ticks), workgroup, aux, 0 — of the last fused launch."""
+        """[units, 6] uint64 of the last fused launch, in its unit order: start, inputs ready, end (100 MHz ticks),
+        workgroup, aux, aux2 (see moe_gpu_trace_units in include/moe_gpu.h)."""
         cap = 1 << 16
         buf = np.zeros((cap, 6), np.uint64); n = C.c_int()
         self._chk(self.L.moe_gpu_read_trace(self.h, _p(buf), cap, C.byref(n)))

@@ -474,6 +474,37 @@ def test_solar_shared_ksplit_paths_and_bars(solar, kp, kps):
         tier.set_option(OPT_KSPLIT_SHARED, 0)
 
 
+def test_solar_unit_trace(solar):
+    """The fused kernel's unit trace: one record per unit of the work list, stamps in order within each unit (down
+    units: act staged, then stream done; the tile's combining unit: other terms in after its stream), and tracing
+    leaves the output bits unchanged."""
+    from moe_gpu import OPT_LAST_GRID
+    tier, hl = solar
+    x = random_x(1, SOLAR.H, np.random.default_rng(170))
+    say("solar unit trace T=1")
+    base, _, _ = tier.layer(0, x)
+    try:
+        tier.trace_units(True)
+        out, _, _ = tier.layer(0, x)
+        tr = tier.read_trace().astype(np.int64)
+        grid = tier.get_option(OPT_LAST_GRID)
+    finally:
+        tier.trace_units(False)
+    np.testing.assert_array_equal(out.view(np.uint32), base.view(np.uint32))
+    nR, maxs, S, nht, ntile, kp = (SOLAR.E + 3) // 4, SOLAR.n_shared + SOLAR.k, SOLAR.n_shared, SOLAR.H // 64, \
+        SOLAR.F // 32, 2
+    assert tr.shape == (nR + 1 + maxs * ntile * kp + maxs * nht, 6)
+    start, ready, end, wg, aux, aux2 = tr.T
+    assert np.all(start > 0) and np.all(end >= start)
+    assert np.all((wg >= 0) & (wg < grid))
+    down = aux2 > 0
+    assert down.sum() == maxs * nht
+    assert np.all(start[down] <= aux[down]) and np.all(aux[down] <= aux2[down]) and np.all(aux2[down] <= end[down])
+    comb = down & (ready > 0)
+    assert comb.sum() == nht  # one combining unit per output tile (folded at T=1)
+    assert np.all(aux2[comb] <= ready[comb]) and np.all(ready[comb] <= end[comb])
+
+
 def test_fused_calls_interleaved_with_route_calls(solar):
     """Route-only calls between fused layer calls (they take call tags but run no fused kernel) must not disturb the
     fused kernel's work queue: every layer call gives the first call's bits."""
