@@ -254,6 +254,8 @@ def main():
         "host_buffer_us_per_call": round(host_us, 2),
         "algorithmic_bytes_per_step": int(avg_bytes), "event_ms_per_step": round(ev_ms / K, 5),
         "decode_layer_calls_per_s": round(1e3 / ms_per_step, 1),
+        # the MoE blocks of a 48-layer Solar decode step alone (attention and LM head are not part of this path)
+        "decode_tokens_per_s_moe_blocks_48_layers": round(T * 1e3 / (48 * ms_per_step), 1),
         "config": {"workload": w.name, "H": w.H, "F": w.F, "E": w.E, "topk": w.k, "n_shared": w.n_shared,
                    "tokens": T, "keep": keep, "resident_layers": L, "distinct_experts_avg": float(np.mean(distinct))},
         "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
