@@ -13,7 +13,7 @@ import pytest
 
 import oracle as O
 from moe_gpu import ACCUMULATE, EINVAL, ESTATE, INT8, MoeGpu, MoeGpuError, gpu_moe, synth_c
-from moe_gpu.workloads import SOLAR, SOLAR_INT8, TINY, solar_batch
+from moe_gpu.workloads import SOLAR, SOLAR_INT8, TINY, Workload, solar_batch
 from moe_ref import HostLayer, assert_layer_close, oracle_layer, random_layer, random_x, upload
 
 pytestmark = pytest.mark.gpu
@@ -171,6 +171,39 @@ def test_synth_fill_matches_host_generator():
         got = buf.cpu().numpy().view(np.uint16)
         np.testing.assert_array_equal(got, O.synth_bf16(key, n, c, start=4096))
     finally:
+        tier.close()
+
+
+# ------------------------------------------------------------------------------------------------ another shape
+MEDIUM = Workload("medium: H=1536 E=40+2 shared top-6 F=768", 1536, 768, 40, 6, 2, zipf_s=1.1, seed=21)
+
+
+def test_medium_shape_two_shared_experts():
+    """A shape unlike both configs (two shared experts, top-6 of 40, H=1536, F=768, a biased router): routing
+    bit-exact, bf16 and int8 (keep 3) outputs within the bars, fused == unfused bit for bit."""
+    from moe_gpu import OPT_FUSED
+    rng = np.random.default_rng(180)
+    say("medium: upload numpy-normal weights H=1536 F=768 E=40+2 k=6")
+    hl = random_layer(MEDIUM, rng)  # its router bias: log-Zipf(1.1) ranks, seed 21
+    tier = MoeGpu(MEDIUM.H, MEDIUM.F, MEDIUM.E, MEDIUM.k, MEDIUM.n_shared, n_layers=1, max_tokens=8)
+    try:
+        upload(tier, hl)
+        tier.quantize_layer(0)
+        for T in (1, 3, 8):
+            x = random_x(T, MEDIUM.H, rng)
+            for flags, keep in ((0, 0), (INT8, 3)):
+                say(f"medium T={T} flags={flags}")
+                ref = oracle_layer(hl, x, keep=keep, int8=bool(flags))
+                tier.set_option(OPT_FUSED, 1)
+                of, idf, gf = tier.layer(0, x, keep=keep, flags=flags)
+                tier.set_option(OPT_FUSED, 0)
+                ou, idu, _ = tier.layer(0, x, keep=keep, flags=flags)
+                check_route(idf, gf, ref, keep or MEDIUM.k)
+                np.testing.assert_array_equal(idf, idu)
+                np.testing.assert_array_equal(of.view(np.uint32), ou.view(np.uint32))
+                assert_layer_close(of, ref["out"])
+    finally:
+        tier.set_option(OPT_FUSED, 1)
         tier.close()
 
 
