@@ -286,19 +286,19 @@ int next_epoch(moe_gpu* c, unsigned* ep) {
     return MOE_GPU_OK;
 }
 
-// K parts per gate|up tile: the option, else about 256 KiB of weights per part (64 rows x H / kp), the size that
-// measured best for the fused schedule at H = 4096 (smaller parts add per-unit latency, larger ones a longer tail).
-static int kparts_for(size_t tile) {
+// K parts per gate|up tile: the option, else about 128 K weights per part (64 rows x H / kp; 256 KiB of bf16, 128 KiB
+// of int8), the size that measured best for the fused schedule at H = 4096 in both precisions (smaller parts add
+// per-unit latency, larger ones a longer tail).
+static int kparts_auto(int H) {
+    const size_t weights = (size_t)64 * H;
     int kp = 1;
-    while (kp < moe::kMaxKp && tile / (kp * 2) >= ((size_t)256 << 10)) kp *= 2;
+    while (kp < moe::kMaxKp && weights / (kp * 2) >= ((size_t)128 << 10)) kp *= 2;
     return kp;
 }
-static int kparts(const moe_gpu* c, bool int8) {
-    return c->ksplit > 0 ? c->ksplit : kparts_for((size_t)64 * c->d.H * (int8 ? 1 : 2));
-}
-// The shared experts stay bf16 in an int8 call: their parts are sized by their own bytes.
+static int kparts(const moe_gpu* c) { return c->ksplit > 0 ? c->ksplit : kparts_auto(c->d.H); }
+// The shared experts' parts (bf16 in every call) can be set apart from the routed experts'.
 static int kparts_shared(const moe_gpu* c) {
-    return c->ksplit_shared > 0 ? c->ksplit_shared : kparts_for((size_t)64 * c->d.H * 2);
+    return c->ksplit_shared > 0 ? c->ksplit_shared : kparts_auto(c->d.H);
 }
 
 // The expert pipeline of one call.  do_topk: route on the device from the layer's router (ids/gates are outputs);
@@ -315,7 +315,7 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
     a.x = x; a.out = out; a.ids = ids; a.gates = gates;
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
-    a.kp = kparts(c, a.int8 != 0);
+    a.kp = kparts(c);
     a.kps = kparts_shared(c);
     a.gpart = c->d_gpart;
     if ((rc = next_epoch(c, &a.epoch))) return rc;
