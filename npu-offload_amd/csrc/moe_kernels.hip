@@ -1039,7 +1039,7 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
 // ====================================================================================================================
 // Fused path: one persistent kernel walks the unit list
 //   [router units][route publisher][shared slots' gate|up parts][the first routed gate|up blocks]
-//   [shared slots' downs][routed gate|up and down blocks][remaining routed downs]
+//   [shared slots' downs][more routed gate|up blocks, then gate|up and down blocks][remaining routed downs]
 // A slot's gate|up block holds its F/32 tiles x kp K parts (parts of a tile adjacent, the finishing part last); its
 // down block holds its H/64 down tiles.  Routed slot s's gate|up block is followed by routed slot (s - lag)'s down
 // block, so a down unit is handed out about lag blocks after the gate|up units it reads.  Workgroup b runs units b and grid + b
@@ -1054,7 +1054,7 @@ struct UnitRef {
     int kind;  // 0 router, 1 publisher, 2 gate|up part, 3 down tile
     int sl, idx;
 };
-__device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int gs, int g, int nht, int lag) {
+__device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int gs, int g, int nht, int lag, int grid) {
     if (u < uR) return {0, 0, u};
     u -= uR;
     if (u < 1) return {1, 0, 0};
@@ -1063,13 +1063,17 @@ __device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int 
     u -= S * gs;
     const int Mr = M - S;               // routed slots S .. M - 1, numbered r = slot - S below
     const int n0 = min(lag, Mr);        // gate|up-only blocks: r = 0 .. n0 - 1
-    if (u < n0 * g) return {2, S + u / g, u % g};
-    u -= n0 * g;
-    // the shared slots' downs follow the first routed gate|up blocks: queued earlier, their workgroups would sit
-    // waiting for the shared act rows while the routed parts wait for workgroups (measured 0.7 us slower at Solar
-    // batch 1, 2 us at int8)
+    // The shared slots' downs come after the first nx routed gate|up blocks, about 1.25 grids of units: queued
+    // right after the shared gate|up parts, their workgroups sat waiting for the shared act rows while routed parts
+    // waited for workgroups (0.7 us slower at Solar batch 1, 2 us for int8); after 4 of Solar's 8 blocks measured
+    // 0.35 us faster than after all 8, after 2 or 6 slower.
+    const int nx = min(n0, max(1, (5 * grid / 4 + g - 1) / g));
+    if (u < nx * g) return {2, S + u / g, u % g};
+    u -= nx * g;
     if (u < S * nht) return {3, u / nht, u % nht};
     u -= S * nht;
+    if (u < (n0 - nx) * g) return {2, S + nx + u / g, u % g};
+    u -= (n0 - nx) * g;
     const int n1 = max(0, Mr - lag);    // paired steps i: gate|up of r = lag + i, then down of r = i
     if (u < n1 * (g + nht)) {
         const int i = u / (g + nht), w = u % (g + nht);
@@ -1126,7 +1130,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
             else next = 2 * grid + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
         }
-        const UnitRef ur = decode_unit(u, f.nR, S, maxs, gs, g, nht, f.lag);
+        const UnitRef ur = decode_unit(u, f.nR, S, maxs, gs, g, nht, f.lag, grid);
         uint64_t t_ready = 0, t_aux = 0, t_aux2 = 0;
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
