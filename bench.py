@@ -246,7 +246,8 @@ def main():
 
     us_tok = ms_per_step * 1e3 / T
     line = {
-        "metric": METRIC, "value": round(us_tok, 2), "unit": "us/layer/token", "n_gpus": 1, "steps": K, "warmup": W,
+        "metric": METRIC if args.workload == "solar" else METRIC.replace("bf16 batch 1", f"{args.workload} workload"),
+        "value": round(us_tok, 2), "unit": "us/layer/token", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8w-bf16" if w.int8 else "bf16", "data": "synthetic (seeded, weights ~N(0,0.02), x ~N(0,1))",
         "achieved_TBps": round(achieved / 1e3, 3), "hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
