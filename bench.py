@@ -93,6 +93,105 @@ def cpu_baseline(w: Workload, budget_s: float = 12.0) -> dict | None:
                       f"{ne}-expert pool + router GEMV/top-k), median; {'cpu_kern.c ck_gemv+ck_moe3' if kind == 'reference' else 'scalar restatement'}"}
 
 
+LM_HEAD_H, LM_HEAD_V = 4096, 196608
+LM_HEAD_METRIC = "LM head (final RMSNorm + GEMV over V=196608 + greedy argmax) µs/token + achieved HBM TB/s, bf16 batch 1"
+
+
+def cpu_baseline_lm_head(budget_s: float = 10.0) -> dict | None:
+    """The reference host step's tail timed on this host: rmsnorm (host.rs:71-76, restated) + ck_gemv over the
+    [196608, 4096] table (cpu_kern.c:32, the reference's own build) + the first-maximum loop (main.rs:384-385)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    if not O.ref_available():
+        return None
+    H, V = LM_HEAD_H, LM_HEAD_V
+    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    R = O.Ref()
+    R.set_threads(cores)
+    blk = O.f2bf(np.random.default_rng(0).normal(0, 0.02, (64, H)).astype(np.float32))
+    W = np.empty((V, H), np.uint16)
+    for r in range(0, V, 64):
+        W[r:r + 64] = blk
+    wf = O.f2bf(np.ones(H, np.float32))
+    x = O.f2bf(np.random.default_rng(1).normal(0, 1, H).astype(np.float32))
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while (len(ts) < 5 or time.perf_counter() < t_end) and len(ts) < 200:
+        t0 = time.perf_counter()
+        hn = O.rmsnorm(x, wf)
+        lg = R.gemv(W, hn)
+        int(np.argmax(lg))
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts[1:])
+    return {"value": round(med * 1e6, 1), "unit": "us/token", "cores": cores, "kind": "reference",
+            "GBps": round(V * H * 2 / med / 1e9, 1),
+            "sample": f"{len(ts) - 1} decode-step tails (rmsnorm + cpu_kern.c ck_gemv over the 1.61 GB table + "
+                      f"argmax), median"}
+
+
+def bench_lm_head(args) -> None:
+    """The step's tail on the GPU: moe_head_argmax_dev on one token, the 1.61 GB table resident in HBM (no layer
+    rotation is needed: the table is six times the size of the Infinity Cache)."""
+    import torch
+
+    from moe_gpu import LmHead
+
+    H, V, K, W_ = LM_HEAD_H, LM_HEAD_V, args.steps, args.warmup
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    log("lm-head: draw the table on the device")
+    g = torch.Generator(device=dev).manual_seed(0)
+    Wt = (torch.randn(V, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    wf = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(torch.bfloat16)
+    P = 16
+    xs = torch.randn(P, H, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    ids = torch.zeros(K + W_, dtype=torch.int32, device=dev)
+    best = torch.zeros(K + W_, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    head = LmHead(H, V)
+    head.load_dev(Wt.view(torch.int16), wf.view(torch.int16))
+    del Wt
+    torch.cuda.empty_cache()
+    head.set_stream(stream)
+    log(f"warmup {W_} steps")
+    for i in range(W_):
+        head.argmax_dev(1, xs[i % P], ids[i:i + 1], best[i:i + 1])
+    torch.cuda.synchronize()
+    log(f"timing {K} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        head.argmax_dev(1, xs[i % P], ids[W_ + i:W_ + i + 1], best[W_ + i:W_ + i + 1])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_ms = e0.elapsed_time(e1)
+    nbytes = V * H * 2
+    ev_us = ev_ms / K * 1e3
+    achieved = nbytes / (ev_us * 1e-6) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_lm_head()
+    traffic = measured_traffic("head_kernel", "lm-head")
+    line = {
+        "metric": LM_HEAD_METRIC, "value": round(wall_ms * 1e3 / K, 2), "unit": "us/token", "n_gpus": 1, "steps": K,
+        "warmup": W_, "ms_per_step": round(wall_ms / K, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded, weights ~N(0,0.02), x ~N(0,1))",
+        "event_ms_per_step": round(ev_ms / K, 5),
+        "config": {"workload": "lm-head: final RMSNorm + LM head H=4096 V=196608 + argmax, bf16, batch 1",
+                   "H": H, "V": V, "tokens": 1},
+        "roofline": {"kernel": "head_kernel", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "bytes_per_launch": nbytes, "avg_us": round(ev_us, 2),
+                     "timing": "timed-region hipEvents on the head's stream; each step is head_kernel + a one-wave "
+                               "finish kernel, so achieved slightly understates the GEMV kernel's own rate"},
+        "cpu_baseline": cpu,
+    }
+    head.close()
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` on bench workload `workload` from the committed rocprofv3 counter summary
     (profiles/<kernel>_<workload>_traffic.txt, line `traffic_bytes_per_launch: N`), or None."""
@@ -112,7 +211,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head"])
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
@@ -124,6 +223,10 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (the expert tier would shard by expert "
               "across GPUs, which is designed but not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "lm-head":
+        bench_lm_head(args)
+        return
 
     import torch
 

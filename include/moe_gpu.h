@@ -158,6 +158,33 @@ int moe_gpu_profile_slots(void);
 int moe_gpu_profile_read(moe_gpu* ctx, int kernel, double* total_ms, int* launches, const char** name);
 int moe_gpu_profile_reset(moe_gpu* ctx);
 
+/* ----------------------------------------------------------------------------------------------- LM head
+ * The step's tail after the last layer: final RMSNorm, LM-head GEMV over the vocabulary, greedy argmax.  Replaces the
+ * host step's `rmsnorm(x, model.norm.weight)`, `gemv(lm_head.weight)` and first-maximum loop
+ * (track2_opt/solar_engine/src/main.rs:381-386, host.rs:71-76) and the chip's lm_head_am + best_key
+ * (src/dense/lm_head.rs:174-181, src/chip.rs:183-194).  Its own context: the table is [V, H] bf16 (1.61 GB for
+ * V = 196608, H = 4096) and is streamed once per call for up to 4 tokens.
+ *   hn[t] = bf16(bf16(x[t] * r) * w_final), r = 1 / sqrt(sum(x[t]^2) / H + eps)   (fp32; sum order is the GPU's)
+ *   logit[t, v] = sum_h W[v, h] * hn[t, h]   (fp32 accumulation of bf16 products)
+ *   ids[t] = the row of the largest logit, exact ties -> lowest row; best[t] its value.  MOE_HEAD_ARGMAX_FP32 compares
+ *   the fp32 logits (main.rs:384-385), MOE_HEAD_ARGMAX_BF16 the logits rounded to bf16 (chip.rs:183-194).
+ * Constraints: H % 1024 == 0, 1024 <= H <= 16384, V >= 1, 1 <= T <= 64. */
+typedef struct moe_head moe_head;
+#define MOE_HEAD_ARGMAX_FP32 0
+#define MOE_HEAD_ARGMAX_BF16 1
+int moe_head_create(int device, int H, int V, float eps, moe_head** out);
+void moe_head_destroy(moe_head* h);
+const char* moe_head_last_error(const moe_head* h); /* h == NULL: the last failed create */
+int moe_head_set_stream(moe_head* h, void* stream);
+int moe_head_synchronize(moe_head* h);
+/* w_lm [V, H] bf16 row-major (lm_head.weight), w_final [H] bf16 (model.norm.weight); host or device pointers */
+int moe_head_load(moe_head* h, const uint16_t* w_lm, const uint16_t* w_final);
+int moe_head_load_dev(moe_head* h, const uint16_t* w_lm, const uint16_t* w_final);
+/* x [T, H] bf16 residual stream; ids [T]; best [T]; logits [T, V] fp32 or NULL.  Host pointers, synchronous. */
+int moe_head_argmax(moe_head* h, int T, const uint16_t* x, int rule, int32_t* ids, float* best, float* logits);
+/* The same on device pointers, enqueued on the head's stream and not synchronised. */
+int moe_head_argmax_dev(moe_head* h, int T, const uint16_t* x, int rule, int32_t* ids, float* best, float* logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,7 +36,10 @@ SYMBOLS = (
     "moe_gpu_synth_layer", "moe_gpu_synth_fill", "moe_gpu_synth_key", "moe_gpu_enable_timing", "moe_gpu_last_time_ms",
     "moe_gpu_set_option", "moe_gpu_get_option", "moe_gpu_trace_units", "moe_gpu_read_trace",
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
+    "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
+    "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
 )
+ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
 
 _lib = None
@@ -108,6 +111,15 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_gpu_profile_slots": (i, []),
         "moe_gpu_profile_read": (i, [vp, i, C.POINTER(C.c_double), C.POINTER(i), C.POINTER(C.c_char_p)]),
         "moe_gpu_profile_reset": (i, [vp]),
+        "moe_head_create": (i, [i, i, i, f, C.POINTER(vp)]),
+        "moe_head_destroy": (None, [vp]),
+        "moe_head_last_error": (C.c_char_p, [vp]),
+        "moe_head_set_stream": (i, [vp, vp]),
+        "moe_head_synchronize": (i, [vp]),
+        "moe_head_load": (i, [vp, vp, vp]),
+        "moe_head_load_dev": (i, [vp, vp, vp]),
+        "moe_head_argmax": (i, [vp, i, vp, i, vp, vp, vp]),
+        "moe_head_argmax_dev": (i, [vp, i, vp, i, vp, vp, vp]),
     }
     for name in SYMBOLS:
         fn = getattr(L, name)
@@ -338,6 +350,65 @@ class MoeGpu:
 
     def route_dev(self, layer: int, T: int, x, ids, gates, logits=None, keep: int = 0):
         self._chk(self.L.moe_gpu_route_dev(self.h, layer, T, _p(x), keep, _p(ids), _p(gates), _p(logits)))
+
+
+class LmHead:
+    """The decode step's tail on the GPU: final RMSNorm, LM-head GEMV, greedy argmax (main.rs:381-386; the chip's
+    lm_head_am + best_key, dense/lm_head.rs:174-181 and chip.rs:183-194).  ``argmax`` returns (ids, best values)
+    and, with ``want_logits``, the fp32 logits [T, V]."""
+
+    def __init__(self, H: int, V: int, eps: float = 1e-5, device: int = 0):
+        self.L = load_library()
+        h = C.c_void_p()
+        rc = self.L.moe_head_create(device, H, V, eps, C.byref(h))
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_head_last_error(None).decode())
+        self.h, self.H, self.V = h, H, V
+
+    def _chk(self, rc: int):
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_head_last_error(self.h).decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.moe_head_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream) -> None:
+        self._chk(self.L.moe_head_set_stream(self.h, getattr(stream, "cuda_stream", stream)))
+
+    def synchronize(self):
+        self._chk(self.L.moe_head_synchronize(self.h))
+
+    def load(self, w_lm, w_final):
+        """Host arrays: w_lm uint16 [V, H] (lm_head.weight bf16 bits), w_final uint16 [H] (model.norm.weight)."""
+        w_lm, w_final = _u16(w_lm), _u16(w_final)
+        assert w_lm.shape == (self.V, self.H) and w_final.shape == (self.H,)
+        self._chk(self.L.moe_head_load(self.h, _p(w_lm), _p(w_final)))
+
+    def load_dev(self, w_lm, w_final):
+        """Device tensors (bf16 or int16 views of bf16 bits) of the same shapes."""
+        assert tuple(w_lm.shape) == (self.V, self.H) and tuple(w_final.shape) == (self.H,)
+        self._chk(self.L.moe_head_load_dev(self.h, _p(w_lm), _p(w_final)))
+
+    def argmax(self, x, rule: int = ARGMAX_FP32, want_logits: bool = False):
+        x = _u16(x).reshape(-1, self.H)
+        T = x.shape[0]
+        ids = np.zeros(T, np.int32)
+        best = np.zeros(T, np.float32)
+        lg = np.zeros((T, self.V), np.float32) if want_logits else None
+        self._chk(self.L.moe_head_argmax(self.h, T, _p(x), rule, _p(ids), _p(best), _p(lg)))
+        return (ids, best, lg) if want_logits else (ids, best)
+
+    def argmax_dev(self, T: int, x, ids, best, logits=None, rule: int = ARGMAX_FP32):
+        """Device pointers; enqueued on the head's stream, not synchronised."""
+        self._chk(self.L.moe_head_argmax_dev(self.h, T, _p(x), rule, _p(ids), _p(best), _p(logits)))
 
 
 def gpu_moe(tier: MoeGpu, layer: int, x, experts: Sequence[int], toks: Sequence, ws: Sequence) -> np.ndarray:

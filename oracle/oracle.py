@@ -11,7 +11,8 @@ three libraries built by ``oracle/Makefile``:
 
 Function names follow the reference: ``cpu_moe`` (cpu_moe.cpp:38), ``ck_moe3`` (cpu_kern.c:141), ``gemv``
 (cpu_kern.c:32), ``quant_row``/``quant_expert`` (cpu_kern.c:218, :227), ``moe_q8w`` (cpu_kern.c:306), ``route``
-(host.rs.tpl:247), ``group_tokens`` (runtime.py:344-347).
+(host.rs.tpl:247), ``group_tokens`` (runtime.py:344-347), ``rmsnorm`` (host.rs:71-76), ``lm_head_argmax``
+(main.rs:384-385, chip.rs:183-194).
 """
 from __future__ import annotations
 
@@ -174,6 +175,26 @@ def route(logits: np.ndarray, bias: np.ndarray | None, k: int, keep: int | None 
     b = np.ascontiguousarray(bias, np.float32) if bias is not None else None
     lib().or_route_softmax(T, E, k, keep or k, logits, b.ctypes.data if b is not None else None, ids, gates)
     return ids, gates
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """host.rs:71-76 (HF SolarOpenRMSNorm): ms = sum(x^2) / H summed in fp32 left to right, r = 1 / sqrt(ms + eps),
+    out = bf16(bf16(x * r) * w).  x: bf16 bits [H] (the residual, bf16 values); w: bf16 bits [H] -> bf16 bits [H]."""
+    xf = bf2f(x).astype(np.float32)
+    ms = np.cumsum(xf * xf, dtype=np.float32)[-1] / np.float32(xf.size)
+    r = np.float32(1.0) / np.sqrt(np.float32(ms + np.float32(eps)))
+    return f2bf(bf2f(f2bf(xf * r)) * bf2f(w))
+
+
+def lm_head_argmax(logits: np.ndarray, rule: int = 0):
+    """Greedy pick over one token's logits [V]: rule 0 compares the fp32 logits and keeps the first maximum
+    (main.rs:384-385); rule 1 compares them rounded to bf16, exact ties -> lowest row (chip.rs:183-194).
+    Returns (row, value compared)."""
+    v = np.ascontiguousarray(logits, np.float32)
+    if rule:
+        v = bf2f(f2bf(v))
+    i = int(np.argmax(v))
+    return i, float(v[i])
 
 
 def group_tokens(ids: np.ndarray, gates: np.ndarray, keep: int | None = None):

@@ -325,3 +325,42 @@ def test_synth_generator_distribution_and_offsets():
     tail = O.synth_bf16(key, 1000, c, start=5000)
     np.testing.assert_array_equal(tail, O.synth_bf16(key, 6000, c)[5000:])
     assert O.synth_key(5, 99) != O.synth_key(5, 100) != O.synth_key(6, 99)
+
+
+# ----------------------------------------------------------------------------- final RMSNorm + LM-head argmax
+def test_rmsnorm_hand_values():
+    # x = [3, 4], eps 0: ms = 12.5, x * r = [0.848528.., 1.131370..] -> bf16 0.84765625 (1 + 89/128) / 2 and
+    # 1.1328125 (1 + 17/128); w = [1, 2] scales exactly.
+    x = O.f2bf(np.array([3.0, 4.0], np.float32))
+    w = O.f2bf(np.array([1.0, 2.0], np.float32))
+    out = O.bf2f(O.rmsnorm(x, w, eps=0.0))
+    assert out.tolist() == [0.84765625, 2.265625]
+    # eps enters under the root: x = [0, 0] gives 0 for any eps; x = [1, 1] with eps = 3 gives r = 1/2
+    assert O.bf2f(O.rmsnorm(O.f2bf(np.ones(2, np.float32)), O.f2bf(np.ones(2, np.float32)), eps=3.0)).tolist() == [0.5, 0.5]
+    assert O.bf2f(O.rmsnorm(np.zeros(4, np.uint16), O.f2bf(np.ones(4, np.float32)), eps=1e-5)).tolist() == [0.0] * 4
+
+
+def test_rmsnorm_close_to_float64_and_scale_invariant():
+    rng = np.random.default_rng(5)
+    H = 4096
+    x = O.f2bf(rng.standard_normal(H).astype(np.float32) * 3)
+    w = O.f2bf((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    out = O.bf2f(O.rmsnorm(x, w))
+    xf = O.bf2f(x).astype(np.float64)
+    ref = xf / np.sqrt(np.mean(xf * xf) + 1e-5) * O.bf2f(w).astype(np.float64)
+    # two bf16 roundings, each within 2^-8 relative (7 stored mantissa bits)
+    rel = np.abs(out - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 2.0 ** -7 + 1e-6 and np.median(rel) < 2.0 ** -8
+    # without eps, doubling x doubles the root exactly: bit-identical output (a wrong mean or a dropped root fails
+    # the float64 check above; a dropped x factor fails this one)
+    x2 = O.f2bf(O.bf2f(x) * 2)
+    assert np.array_equal(O.rmsnorm(x, w, eps=0.0), O.rmsnorm(x2, w, eps=0.0))
+
+
+def test_lm_head_argmax_rules():
+    lg = np.array([0.5, 1.0, 1.0009765625, 1.0009765625, -3.0], np.float32)
+    # fp32: 1 + 2^-10 at rows 2 and 3, first maximum -> 2
+    assert O.lm_head_argmax(lg, 0) == (2, 1.0009765625)
+    # bf16: rows 1..3 all round to 1.0 (ulp 2^-7): tie -> lowest row 1
+    assert O.lm_head_argmax(lg, 1) == (1, 1.0)
+    assert O.lm_head_argmax(np.array([-2.0, -1.0, -1.0], np.float32), 0) == (1, -1.0)
