@@ -172,6 +172,17 @@ def bench_lm_head(args) -> None:
     nbytes = V * H * 2
     ev_us = ev_ms / K * 1e3
     achieved = nbytes / (ev_us * 1e-6) / 1e9
+    if args.copy_calibration > 0:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {args.copy_calibration} MiB")
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = None if args.no_cpu_baseline else cpu_baseline_lm_head()
     traffic = measured_traffic("head_kernel", "lm-head")
     line = {

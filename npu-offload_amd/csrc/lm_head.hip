@@ -18,8 +18,17 @@ namespace {
 
 constexpr int kHeadMaxT = 4;  // tokens per launch; more tokens take several launches
 constexpr int kWaves = 4;     // 256 threads
-constexpr int kRB = 8;        // rows per wave step
-constexpr int kCG = 2;        // 16-byte chunks per lane per load group: a row of H bf16 is H / 512 chunks per lane
+// A wave step covers RB rows, loaded CG 16-byte chunks per lane at a time (a row of H bf16 is H / 512 chunks per
+// lane): <8, 2> for any H % 1024 == 0, <HEAD_RB, HEAD_CG> when H % (512 * HEAD_CG) == 0.  At V = 196608, H = 4096
+// (one token, pipelined loads): 4 whole rows per step 244.8 us, 2 / 3 / 5 rows 251.3 / 249.9 / 248.8 us, 8 rows of
+// 2 KiB slices 279.5 us, 8 rows of 4 KiB 286.5 us.
+constexpr int kRB = 8, kCG = 2;
+#ifndef HEAD_RB
+#define HEAD_RB 4
+#endif
+#ifndef HEAD_CG
+#define HEAD_CG 8
+#endif
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
@@ -71,7 +80,7 @@ __global__ void head_finish(HeadArgs a) {
 // byte read, served by L2), then its waves take steps of kRB consecutive rows, grid-strided over the table.  Lane l
 // reads 16-byte chunks l, l + 64, ... of each row (one wave load = 1 KiB of a row), multiplies them with the same
 // chunks of the normalised tokens from LDS and keeps fp32 partial sums; a butterfly sums the 64 lanes.
-template <int NT>
+template <int NT, int RB, int CG>
 __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
     extern __shared__ __align__(16) uint16_t hn[];  // [NT][H] bf16
     __shared__ float red[NT][kWaves];
@@ -108,55 +117,71 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) best[t] = 0ull;
 
-    for (int r0 = gw * kRB; r0 < V; r0 += nw * kRB) {
-        float acc[NT][kRB];
+    // The wave walks its load groups in order (c0 over a row step's chunks, then its next row step); the next
+    // group's loads are issued as soon as the current group's products are done, so they are in flight during the
+    // step's butterfly and argmax.
+    u32x4 wq[RB][CG];
+    float acc[NT][RB];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int r = 0; r < kRB; ++r) acc[t][r] = 0.f;
-        for (int c0 = 0; c0 < nch; c0 += kCG) {
-            u32x4 wq[kRB][kCG];
+        for (int r = 0; r < RB; ++r) acc[t][r] = 0.f;
+    auto load_group = [&](int r0_, int c0_) {
 #pragma unroll
-            for (int r = 0; r < kRB; ++r) {
-                const int row = r0 + r < V ? r0 + r : V - 1;  // rows past V re-read the last row; discarded below
-                const u32x4* wr = reinterpret_cast<const u32x4*>(a.w + (size_t)row * H);
+        for (int r = 0; r < RB; ++r) {
+            const int row = r0_ + r < V ? r0_ + r : V - 1;  // rows past V re-read the last row; discarded below
+            const u32x4* wr = reinterpret_cast<const u32x4*>(a.w + (size_t)row * H);
 #pragma unroll
-                for (int c = 0; c < kCG; ++c) wq[r][c] = __builtin_nontemporal_load(&wr[(c0 + c) * 64 + lane]);
+            for (int c = 0; c < CG; ++c) wq[r][c] = __builtin_nontemporal_load(&wr[(c0_ + c) * 64 + lane]);
+        }
+    };
+    int r0 = gw * RB, c0 = 0;
+    if (r0 < V) load_group(r0, 0);
+    while (r0 < V) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const u32x4 h4 = *reinterpret_cast<const u32x4*>(&hn[t * H + ((c0 + c) * 64 + lane) * 8]);
+                const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const uint32_t ww[4] = {wq[r][c].x, wq[r][c].y, wq[r][c].z, wq[r][c].w};
+                    float s = acc[t][r];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        s = fmaf(__uint_as_float(ww[j] << 16), __uint_as_float(hw[j] << 16), s);
+                        s = fmaf(__uint_as_float(ww[j] & 0xFFFF0000u), __uint_as_float(hw[j] & 0xFFFF0000u), s);
+                    }
+                    acc[t][r] = s;
+                }
             }
+        }
+        int nr0 = r0, nc0 = c0 + CG;
+        if (nc0 >= nch) {
+            nc0 = 0;
+            nr0 = r0 + nw * RB;
+        }
+        if (nr0 < V) load_group(nr0, nc0);
+        if (nc0 == 0) {  // row step r0 complete
 #pragma unroll
-            for (int c = 0; c < kCG; ++c) {
+            for (int t = 0; t < NT; ++t) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const u32x4 h4 = *reinterpret_cast<const u32x4*>(&hn[t * H + ((c0 + c) * 64 + lane) * 8]);
-                    const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
-#pragma unroll
-                    for (int r = 0; r < kRB; ++r) {
-                        const uint32_t ww[4] = {wq[r][c].x, wq[r][c].y, wq[r][c].z, wq[r][c].w};
-                        float s = acc[t][r];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            s = fmaf(__uint_as_float(ww[j] << 16), __uint_as_float(hw[j] << 16), s);
-                            s = fmaf(__uint_as_float(ww[j] & 0xFFFF0000u), __uint_as_float(hw[j] & 0xFFFF0000u), s);
-                        }
-                        acc[t][r] = s;
+                for (int r = 0; r < RB; ++r) {
+                    const float tot = wave_sum(acc[t][r]);
+                    acc[t][r] = 0.f;
+                    const int row = r0 + r;
+                    if (row < V && t < T) {
+                        if (a.logits && lane == r) a.logits[(size_t)t * V + row] = tot;
+                        const float v = a.rule ? bf2f(f2bf(tot)) : tot;
+                        const unsigned long long k = key_of(v, row);
+                        best[t] = k > best[t] ? k : best[t];
                     }
                 }
             }
         }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-            for (int r = 0; r < kRB; ++r) {
-                const float tot = wave_sum(acc[t][r]);
-                const int row = r0 + r;
-                if (row < V && t < T) {
-                    if (a.logits && lane == r) a.logits[(size_t)t * V + row] = tot;
-                    const float v = a.rule ? bf2f(f2bf(tot)) : tot;
-                    const unsigned long long k = key_of(v, row);
-                    best[t] = k > best[t] ? k : best[t];
-                }
-            }
-        }
+        r0 = nr0;
+        c0 = nc0;
     }
     if (lane == 0) {
 #pragma unroll
@@ -207,10 +232,10 @@ int hfail(moe_head* h, int code, const char* fmt, ...) {
                          #expr, hipGetErrorString(e_), __FILE__, __LINE__);                                     \
     } while (0)
 
-template <int NT>
+template <int NT, int RB, int CG>
 int head_grid(moe_head* h, size_t lds, int* grid) {
     if (h->grid[NT] == 0) {
-        const void* fn = reinterpret_cast<const void*>(&head_kernel<NT>);
+        const void* fn = reinterpret_cast<const void*>(&head_kernel<NT, RB, CG>);
         int ncu = 0, per_cu = 0;
         HCHK(h, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         HCHK(h, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, h->device));
@@ -218,20 +243,25 @@ int head_grid(moe_head* h, size_t lds, int* grid) {
         if (per_cu < 1) return hfail(h, MOE_GPU_EINVAL, "head kernel does not fit a CU with %zu bytes of LDS", lds);
         h->grid[NT] = ncu * per_cu;
     }
-    const int steps = (h->V + kRB - 1) / kRB;
+    const int steps = (h->V + RB - 1) / RB;
     const int need = (steps + kWaves - 1) / kWaves;
     *grid = h->grid[NT] < need ? h->grid[NT] : need;
     return MOE_GPU_OK;
 }
 
-template <int NT>
-int head_launch(moe_head* h, HeadArgs a) {
+template <int NT, int RB, int CG>
+int head_launch_rc(moe_head* h, HeadArgs a) {
     const size_t lds = (size_t)NT * h->H * sizeof(uint16_t);
     int grid = 0, rc;
-    if ((rc = head_grid<NT>(h, lds, &grid)) != MOE_GPU_OK) return rc;
-    hipLaunchKernelGGL(head_kernel<NT>, dim3(grid), dim3(256), lds, h->stream, a);
+    if ((rc = head_grid<NT, RB, CG>(h, lds, &grid)) != MOE_GPU_OK) return rc;
+    hipLaunchKernelGGL((head_kernel<NT, RB, CG>), dim3(grid), dim3(256), lds, h->stream, a);
     HCHK(h, hipGetLastError());
     return MOE_GPU_OK;
+}
+
+template <int NT>
+int head_launch(moe_head* h, HeadArgs a) {
+    return h->H % (512 * HEAD_CG) == 0 ? head_launch_rc<NT, HEAD_RB, HEAD_CG>(h, a) : head_launch_rc<NT, kRB, kCG>(h, a);
 }
 
 // Launch sequence for tokens [0, T) of device buffers, kHeadMaxT tokens per table pass.
