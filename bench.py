@@ -203,6 +203,77 @@ def bench_lm_head(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+ATTN_NQ, ATTN_NKV, ATTN_D, ATTN_S = 32, 8, 128, 4096
+ATTN_METRIC = "decode attention (GQA 32 q / 8 kv heads, d=128, KV 4096) µs/layer/token + achieved HBM TB/s, bf16 batch 1"
+
+
+def bench_attn(args) -> None:
+    """Decode attention of one token over a layer's KV cache (S = 4096), rotating over 32 distinct caches
+    (537 MB, beyond the Infinity Cache)."""
+    import torch
+
+    from moe_gpu import attn_decode_dev, attn_workspace_bytes
+
+    NQ, NKV, D, S, K, W_ = ATTN_NQ, ATTN_NKV, ATTN_D, ATTN_S, args.steps, args.warmup
+    L = 32
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    g = torch.Generator(device=dev).manual_seed(0)
+    log(f"attn: {L} caches of 2 x [{S}, {NKV}, {D}] bf16")
+    kc = torch.randn(L, S, NKV, D, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    vc = torch.randn(L, S, NKV, D, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    qs = torch.randn(L, NQ, D, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    out = torch.zeros(NQ, D, dtype=torch.int16, device=dev)
+    ws = torch.zeros(attn_workspace_bytes(NQ, S) // 4, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    for i in range(W_):
+        attn_decode_dev(qs[i % L], kc[i % L], vc[i % L], out, ws, NQ, NKV, S, stream=stream)
+    torch.cuda.synchronize()
+    log(f"timing {K} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        attn_decode_dev(qs[i % L], kc[i % L], vc[i % L], out, ws, NQ, NKV, S, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_us = e0.elapsed_time(e1) / K * 1e3
+    nbytes = 2 * S * NKV * D * 2
+    achieved = nbytes / (ev_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+
+        qh, kh, vh = (t[0].cpu().numpy().view(np.uint16) for t in (qs, kc, vc))
+        ts = []
+        for _ in range(5):
+            c0 = time.perf_counter()
+            O.attention(qh, kh, vh, NKV)
+            ts.append(time.perf_counter() - c0)
+        med = statistics.median(ts)
+        cpu = {"value": round(med * 1e6, 1), "unit": "us/layer/token", "cores": 1, "kind": "port",
+               "GBps": round(nbytes / med / 1e9, 2),
+               "sample": "5 calls of the oracle's numpy restatement of main.rs:86-104 (the reference's Rust host "
+                         "attention cannot be built here), median"}
+    line = {
+        "metric": ATTN_METRIC, "value": round(wall_ms * 1e3 / K, 2), "unit": "us/layer/token", "n_gpus": 1,
+        "steps": K, "warmup": W_, "ms_per_step": round(wall_ms / K, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded, q/k/v ~N(0,1))",
+        "event_ms_per_step": round(ev_us / 1e3, 5),
+        "config": {"workload": "attn: GQA decode attention, 32 q / 8 kv heads, d=128, KV 4096, bf16, batch 1",
+                   "n_q_heads": NQ, "n_kv_heads": NKV, "head_dim": D, "kv_len": S, "tokens": 1},
+        "roofline": {"kernel": "attn_scores + attn_pv + attn_out", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_launch": nbytes, "avg_us": round(ev_us, 2),
+                     "timing": "timed-region hipEvents on the call's stream over the three kernels of a call"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` on bench workload `workload` from the committed rocprofv3 counter summary
     (profiles/<kernel>_<workload>_traffic.txt, line `traffic_bytes_per_launch: N`), or None."""
@@ -222,7 +293,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head"])
+    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head", "attn"])
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
@@ -237,6 +308,9 @@ def main():
 
     if args.workload == "lm-head":
         bench_lm_head(args)
+        return
+    if args.workload == "attn":
+        bench_attn(args)
         return
 
     import torch

@@ -28,6 +28,7 @@
 #ifndef MOE_GPU_H
 #define MOE_GPU_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -184,6 +185,20 @@ int moe_head_load_dev(moe_head* h, const uint16_t* w_lm, const uint16_t* w_final
 int moe_head_argmax(moe_head* h, int T, const uint16_t* x, int rule, int32_t* ids, float* best, float* logits);
 /* The same on device pointers, enqueued on the head's stream and not synchronised. */
 int moe_head_argmax_dev(moe_head* h, int T, const uint16_t* x, int rule, int32_t* ids, float* best, float* logits);
+
+/* ----------------------------------------------------------------------------------------------- decode attention
+ * GQA attention of one token over a layer's KV cache, replacing the host step's core (track2_opt/solar_engine/src/
+ * main.rs:86-104): for q head h and kv head h / (NQ / NKV), positions t < S,
+ *   sc[t] = bf16(bf16(q_h . k_t) * scale)  (dot summed left to right in fp32: bit-identical scores),
+ *   p[t] = bf16(exp(sc[t] - max sc) / sum exp(sc - max sc)),  out_h = bf16(sum_t p[t] v_t)  (fp32 sums in the GPU's order).
+ * q [NQ, D] bf16 (after RoPE), k_cache / v_cache [S, NKV, D] bf16 (16-byte aligned), out [NQ, D] bf16; D = 128,
+ * NQ = G * NKV with G in {1, 2, 4, 8}.  Device pointers; enqueued on `stream` (NULL: the null stream), not synchronised.  The
+ * caller passes a device workspace of moe_attn_workspace_bytes() (scores, then per-chunk partials). */
+size_t moe_attn_workspace_bytes(int n_q_heads, int head_dim, int S);
+int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                        const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+const char* moe_attn_last_error(void); /* message of this thread's last failed moe_attn_decode_dev */
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,7 @@ SYMBOLS = (
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
+    "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
 )
 ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
@@ -120,6 +121,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_head_load_dev": (i, [vp, vp, vp]),
         "moe_head_argmax": (i, [vp, i, vp, i, vp, vp, vp]),
         "moe_head_argmax_dev": (i, [vp, i, vp, i, vp, vp, vp]),
+        "moe_attn_workspace_bytes": (C.c_size_t, [i, i, i]),
+        "moe_attn_decode_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, C.c_size_t, vp]),
+        "moe_attn_last_error": (C.c_char_p, []),
     }
     for name in SYMBOLS:
         fn = getattr(L, name)
@@ -409,6 +413,25 @@ class LmHead:
     def argmax_dev(self, T: int, x, ids, best, logits=None, rule: int = ARGMAX_FP32):
         """Device pointers; enqueued on the head's stream, not synchronised."""
         self._chk(self.L.moe_head_argmax_dev(self.h, T, _p(x), rule, _p(ids), _p(best), _p(logits)))
+
+
+def attn_decode_dev(q, k_cache, v_cache, out, workspace, n_q_heads: int, n_kv_heads: int, S: int,
+                    scale: float | None = None, head_dim: int = 128, stream=None) -> None:
+    """GQA decode attention over a KV cache (main.rs:86-104) on device tensors: q [NQ, D], caches [>= S, NKV, D],
+    out [NQ, D] (bf16 bits as int16 or bfloat16), workspace a device buffer of attn_workspace_bytes().  Enqueued on
+    `stream` (a torch stream or raw handle; None: the null stream)."""
+    L = load_library()
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = L.moe_attn_decode_dev(n_q_heads, n_kv_heads, head_dim, S, scale, _p(q), _p(k_cache), _p(v_cache), _p(out),
+                               _p(workspace), ws_bytes, getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, L.moe_attn_last_error().decode())
+
+
+def attn_workspace_bytes(n_q_heads: int, S: int, head_dim: int = 128) -> int:
+    return int(load_library().moe_attn_workspace_bytes(n_q_heads, head_dim, S))
 
 
 def gpu_moe(tier: MoeGpu, layer: int, x, experts: Sequence[int], toks: Sequence, ws: Sequence) -> np.ndarray:

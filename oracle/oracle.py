@@ -12,7 +12,7 @@ three libraries built by ``oracle/Makefile``:
 Function names follow the reference: ``cpu_moe`` (cpu_moe.cpp:38), ``ck_moe3`` (cpu_kern.c:141), ``gemv``
 (cpu_kern.c:32), ``quant_row``/``quant_expert`` (cpu_kern.c:218, :227), ``moe_q8w`` (cpu_kern.c:306), ``route``
 (host.rs.tpl:247), ``group_tokens`` (runtime.py:344-347), ``rmsnorm`` (host.rs:71-76), ``lm_head_argmax``
-(main.rs:384-385, chip.rs:183-194).
+(main.rs:384-385, chip.rs:183-194), ``attention`` (main.rs:86-104).
 """
 from __future__ import annotations
 
@@ -195,6 +195,28 @@ def lm_head_argmax(logits: np.ndarray, rule: int = 0):
         v = bf2f(f2bf(v))
     i = int(np.argmax(v))
     return i, float(v[i])
+
+
+def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_kv: int, scale: float | None = None):
+    """Decode attention of main.rs:86-104 for one token.  q: bf16 bits [NQ, D] (after RoPE); kc, vc: bf16 bits
+    [S, NKV, D].  Per q head h (kv head h // (NQ / NKV)): sc = bf16(bf16(q . k) * scale) with the dot summed left to
+    right in fp32; p = bf16(exp(sc - max) / tot) with tot summed left to right; out = bf16(sum_t p v_t) summed left
+    to right.  Returns (out bf16 bits [NQ, D], scores fp32 [NQ, S])."""
+    q = np.ascontiguousarray(q, np.uint16); NQ, D = q.shape
+    S = kc.shape[0]; G = NQ // n_kv
+    sc32 = np.float32(1.0) / np.sqrt(np.float32(D)) if scale is None else np.float32(scale)
+    qf, kf, vf = bf2f(q), bf2f(kc).reshape(S, n_kv, D), bf2f(vc).reshape(S, n_kv, D)
+    out = np.zeros((NQ, D), np.uint16); scores = np.zeros((NQ, S), np.float32)
+    for h in range(NQ):
+        g = h // G
+        dot = np.cumsum(qf[h][None, :] * kf[:, g, :], axis=1, dtype=np.float32)[:, -1]
+        sc = bf2f(f2bf(bf2f(f2bf(dot)) * sc32))
+        e = np.exp(sc - sc.max()).astype(np.float32)
+        tot = np.cumsum(e, dtype=np.float32)[-1]
+        p = bf2f(f2bf(e / tot))
+        out[h] = f2bf(np.cumsum(p[:, None] * vf[:, g, :], axis=0, dtype=np.float32)[-1])
+        scores[h] = sc
+    return out, scores
 
 
 def group_tokens(ids: np.ndarray, gates: np.ndarray, keep: int | None = None):

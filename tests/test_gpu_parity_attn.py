@@ -1,0 +1,84 @@
+"""GPU parity of decode attention (moe_attn_decode_dev through the C ABI) against the oracle's restatement of
+main.rs:86-104.
+
+Bars:
+  * scores: bit-identical (the GPU sums each q . k left to right in fp32, as the reference);
+  * out (bf16): |gpu - ref| <= 2^-7 |ref| + 1e-3 max|ref| and rel-L2 <= 5e-3.  The softmax total and the P.V sums
+    run in the GPU's order, so a probability or an output can land on the other side of a bf16 rounding boundary;
+  * a one-hot softmax (exact in any order) gives out = v[t*] bit for bit, per kv head of the group mapping.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from moe_gpu import EINVAL, MoeGpuError, attn_decode_dev, attn_workspace_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-attn] {msg}", flush=True)
+
+
+def run_gpu(q, k, v, NKV, S=None):
+    import torch
+
+    NQ = q.shape[0]
+    S = k.shape[0] if S is None else S
+    dev = "cuda:0"
+    qd = torch.from_numpy(q.view(np.int16)).to(dev)
+    kd = torch.from_numpy(k.view(np.int16)).to(dev)
+    vd = torch.from_numpy(v.view(np.int16)).to(dev)
+    od = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    ws = torch.zeros(attn_workspace_bytes(NQ, S) // 4, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    attn_decode_dev(qd, kd, vd, od, ws, NQ, NKV, S)  # null stream: ordered after torch's copies
+    torch.cuda.synchronize()
+    return od.cpu().numpy().view(np.uint16), ws[:NQ * S].cpu().numpy().reshape(NQ, S)
+
+
+def check_out(gpu, ref):
+    g, r = O.bf2f(gpu).astype(np.float64), O.bf2f(ref).astype(np.float64)
+    assert np.all(np.abs(g - r) <= 2.0 ** -7 * np.abs(r) + 1e-3 * np.abs(r).max()), np.abs(g - r).max()
+    assert np.linalg.norm(g - r) <= 5e-3 * np.linalg.norm(r)
+
+
+@pytest.mark.parametrize("NQ,NKV,S", [(32, 8, 4096), (32, 8, 1), (32, 8, 37), (32, 8, 300), (4, 4, 777), (16, 2, 513)])
+def test_attention_matches_oracle(NQ, NKV, S):
+    say(f"attention NQ={NQ} NKV={NKV} S={S}")
+    rng = np.random.default_rng(S + NQ)
+    q = O.f2bf(rng.standard_normal((NQ, 128)).astype(np.float32))
+    k = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    ref, sc = O.attention(q, k, v, NKV)
+    out, gsc = run_gpu(q, k, v, NKV)
+    np.testing.assert_array_equal(gsc.view(np.uint32), sc.view(np.uint32))
+    check_out(out, ref)
+
+
+def test_attention_one_hot_exact():
+    say("attention one-hot")
+    rng = np.random.default_rng(3)
+    NQ, NKV, S = 32, 8, 600
+    q = np.zeros((NQ, 128), np.uint16)
+    q[:, 0] = O.f2bf(np.array([1.0], np.float32))[0]
+    k = O.f2bf((0.01 * rng.standard_normal((S, NKV, 128))).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    star = [0, 255, 256, 599, 300, 1, 511, 512]  # chunk edges
+    for g, t in enumerate(star):
+        k[t, g, 0] = O.f2bf(np.array([2000.0], np.float32))[0]
+    out, _ = run_gpu(q, k, v, NKV)
+    for h in range(NQ):
+        np.testing.assert_array_equal(out[h], v[star[h // 4], h // 4])
+
+
+def test_attention_errors():
+    import torch
+
+    ws = torch.zeros(1024, dtype=torch.float32, device="cuda:0")
+    x = torch.zeros(4096, dtype=torch.int16, device="cuda:0")
+    for args in ((32, 8, 64, 16), (32, 5, 128, 16), (32, 2, 128, 16), (32, 8, 128, 0), (32, 8, 128, 4096)):
+        NQ, NKV, D, S = args
+        with pytest.raises(MoeGpuError) as e:
+            attn_decode_dev(x, x, x, x, ws, NQ, NKV, S, head_dim=D)
+        assert e.value.code == EINVAL

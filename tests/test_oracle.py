@@ -364,3 +364,51 @@ def test_lm_head_argmax_rules():
     # bf16: rows 1..3 all round to 1.0 (ulp 2^-7): tie -> lowest row 1
     assert O.lm_head_argmax(lg, 1) == (1, 1.0)
     assert O.lm_head_argmax(np.array([-2.0, -1.0, -1.0], np.float32), 0) == (1, -1.0)
+
+
+# ----------------------------------------------------------------------------- decode attention (main.rs:86-104)
+def _attn_inputs(rng, NQ, NKV, S, D=128, ksd=1.0):
+    q = O.f2bf(rng.standard_normal((NQ, D)).astype(np.float32))
+    k = O.f2bf((ksd * rng.standard_normal((S, NKV, D))).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, D)).astype(np.float32))
+    return q, k, v
+
+
+def test_attention_close_to_float64_softmax():
+    rng = np.random.default_rng(7)
+    q, k, v = _attn_inputs(rng, 8, 2, 300, ksd=0.3)
+    out, sc = O.attention(q, k, v, 2)
+    qf, kf, vf = (O.bf2f(a).astype(np.float64) for a in (q, k, v))
+    for h in range(8):
+        s = kf[:, h // 4, :] @ qf[h] / np.sqrt(128.0)
+        assert np.max(np.abs(sc[h] - s)) <= 2.0 ** -7 * np.max(np.abs(s)) + 1e-6  # two bf16 roundings
+        p = np.exp(s - s.max()); p /= p.sum()
+        ref = p @ vf[:, h // 4, :]
+        assert np.max(np.abs(O.bf2f(out[h]) - ref)) <= 0.02 * np.max(np.abs(ref)) + 1e-3
+
+
+def test_attention_one_hot_and_group_mapping():
+    # q = e0; key t* of kv head g carries 2000 in dim 0: its score bf16(2000 / sqrt(128)) beats the others by > 150,
+    # so exp underflows to 0 elsewhere, p = 1 there and out = v[t*] exactly.  Each kv head picks its own t*.
+    rng = np.random.default_rng(8)
+    NQ, NKV, S = 8, 4, 50
+    q = np.zeros((NQ, 128), np.uint16); q[:, 0] = O.f2bf(np.array([1.0], np.float32))[0]
+    k = O.f2bf((0.01 * rng.standard_normal((S, NKV, 128))).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    star = [3, 17, 49, 0]
+    for g, t in enumerate(star):
+        k[t, g, 0] = O.f2bf(np.array([2000.0], np.float32))[0]
+    out, _ = O.attention(q, k, v, NKV)
+    for h in range(NQ):
+        assert np.array_equal(out[h], v[star[h // 2], h // 2])
+
+
+def test_attention_equal_keys_give_uniform_weights():
+    rng = np.random.default_rng(9)
+    S = 64
+    q, k, v = _attn_inputs(rng, 2, 1, S)
+    k[:] = k[0]
+    out, sc = O.attention(q, k, v, 1)
+    assert np.all(sc == sc[:, :1])
+    ref = O.bf2f(v).astype(np.float64)[:, 0, :].mean(axis=0)  # p = bf16(1/64) = 1/64 exactly
+    assert np.max(np.abs(O.bf2f(out[0]) - ref)) <= 2.0 ** -8 * np.max(np.abs(ref)) + 1e-6
