@@ -5,7 +5,7 @@
 //   p[t]  = bf16(exp(sc[t] - max sc) / sum exp(sc - max sc))
 //   out_h = bf16(sum_t p[t] * v_t)
 // Three kernels: scores (one lane per position and kv head, the dot in the reference's order, so the scores are
-// bit-identical), softmax + partial P.V per 256-position chunk, and the sum of the chunk partials.  HBM-bound on the
+// bit-identical), softmax + partial P.V per 128-position chunk, and the sum of the chunk partials.  HBM-bound on the
 // cache read: 2 * S * NKV * D * 2 bytes per call (16.8 MB at S = 4096, NKV = 8, D = 128).
 #include <hip/hip_runtime.h>
 
@@ -16,7 +16,14 @@
 namespace {
 
 constexpr int kD = 128;      // head dim
-constexpr int kChunk = 256;  // positions per P.V workgroup
+#ifndef ATTN_CHUNK
+#define ATTN_CHUNK 128
+#endif
+#ifndef ATTN_ST
+#define ATTN_ST 64
+#endif
+constexpr int kChunk = ATTN_CHUNK;  // positions per P.V workgroup
+constexpr int kST = ATTN_ST;        // threads (positions) per score workgroup
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
@@ -37,14 +44,14 @@ struct AttnArgs {
     float scale;
 };
 
-// grid (ceil(S / 256), NKV): thread = one position of kv head blockIdx.y, all G q heads of that kv head.
+// grid (ceil(S / kST), NKV): thread = one position of kv head blockIdx.y, all G q heads of that kv head.
 template <int G>
-__global__ __launch_bounds__(256) void attn_scores(AttnArgs a) {
+__global__ __launch_bounds__(kST) void attn_scores(AttnArgs a) {
     __shared__ float qs[G * kD];
     const int g = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < G * kD; i += 256) qs[i] = bf2f(a.q[(size_t)g * G * kD + i]);
+    for (int i = tid; i < G * kD; i += kST) qs[i] = bf2f(a.q[(size_t)g * G * kD + i]);
     __syncthreads();
-    const int t = blockIdx.x * 256 + tid;
+    const int t = blockIdx.x * kST + tid;
     if (t >= a.S) return;
     const u32x4* kr = reinterpret_cast<const u32x4*>(a.k + ((size_t)t * a.NKV + g) * kD);
     u32x4 kk[kD / 8];
@@ -141,7 +148,8 @@ __global__ __launch_bounds__(256) void attn_pv(AttnArgs a) {
         }
     }
     __syncthreads();
-    {
+    static_assert(kChunk % 64 == 0 && kChunk <= 256, "one p per thread of the first kChunk threads");
+    if (tid < kChunk) {  // whole waves
         float sv[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) sv[h] = sc0[(size_t)h * S + t0 + min(tid, n - 1)];
@@ -239,12 +247,12 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
     AttnArgs a{q, k_cache, v_cache, out, scores, scores + (size_t)n_q_heads * S, n_q_heads, n_kv_heads,
                n_q_heads / n_kv_heads, S, nchunk, scale};
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 gs((S + 255) / 256, n_kv_heads), gp(nchunk, n_kv_heads);
+    const dim3 gs((S + kST - 1) / kST, n_kv_heads), gp(nchunk, n_kv_heads);
     switch (a.G) {
-        case 1: hipLaunchKernelGGL(attn_scores<1>, gs, dim3(256), 0, st, a); hipLaunchKernelGGL(attn_pv<1>, gp, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(attn_scores<2>, gs, dim3(256), 0, st, a); hipLaunchKernelGGL(attn_pv<2>, gp, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(attn_scores<4>, gs, dim3(256), 0, st, a); hipLaunchKernelGGL(attn_pv<4>, gp, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL(attn_scores<8>, gs, dim3(256), 0, st, a); hipLaunchKernelGGL(attn_pv<8>, gp, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL(attn_scores<1>, gs, dim3(kST), 0, st, a); hipLaunchKernelGGL(attn_pv<1>, gp, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(attn_scores<2>, gs, dim3(kST), 0, st, a); hipLaunchKernelGGL(attn_pv<2>, gp, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(attn_scores<4>, gs, dim3(kST), 0, st, a); hipLaunchKernelGGL(attn_pv<4>, gp, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(attn_scores<8>, gs, dim3(kST), 0, st, a); hipLaunchKernelGGL(attn_pv<8>, gp, dim3(256), 0, st, a); break;
     }
     hipLaunchKernelGGL(attn_out, dim3((n_q_heads * kD + 255) / 256), dim3(256), 0, st, a);
     const hipError_t e = hipGetLastError();
