@@ -95,7 +95,18 @@ __global__ __launch_bounds__(256) void attn_pv(AttnArgs a) {
     float m[G], sum[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) m[h] = -INFINITY, sum[h] = 0.f;
-    for (int b0 = 0; b0 < S; b0 += 256 * kSB) {
+    // the first block of scores stays in registers for the second pass (S <= 4096 reads the scores once)
+    float v0[G][kSB];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int u = 0; u < kSB; ++u) {
+            const int t = u * 256 + tid;
+            const float x = sc0[(size_t)h * S + min(t, S - 1)];
+            v0[h][u] = t < S ? x : -INFINITY;
+            m[h] = fmaxf(m[h], v0[h][u]);
+        }
+    for (int b0 = 256 * kSB; b0 < S; b0 += 256 * kSB) {
         float v[G][kSB];
 #pragma unroll
         for (int h = 0; h < G; ++h)
@@ -119,7 +130,12 @@ __global__ __launch_bounds__(256) void attn_pv(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) m[h] = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
     __syncthreads();
-    for (int b0 = 0; b0 < S; b0 += 256 * kSB) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int u = 0; u < kSB; ++u)
+            if (u * 256 + tid < S) sum[h] += expf(v0[h][u] - m[h]);
+    for (int b0 = 256 * kSB; b0 < S; b0 += 256 * kSB) {
         float v[G][kSB];
 #pragma unroll
         for (int h = 0; h < G; ++h)

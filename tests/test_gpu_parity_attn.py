@@ -43,7 +43,8 @@ def check_out(gpu, ref):
     assert np.linalg.norm(g - r) <= 5e-3 * np.linalg.norm(r)
 
 
-@pytest.mark.parametrize("NQ,NKV,S", [(32, 8, 4096), (32, 8, 1), (32, 8, 37), (32, 8, 300), (4, 4, 777), (16, 2, 513)])
+@pytest.mark.parametrize("NQ,NKV,S", [(32, 8, 4096), (32, 8, 1), (32, 8, 37), (32, 8, 300), (4, 4, 777), (16, 2, 513),
+                                      (32, 8, 5000), (16, 2, 9000)])
 def test_attention_matches_oracle(NQ, NKV, S):
     say(f"attention NQ={NQ} NKV={NKV} S={S}")
     rng = np.random.default_rng(S + NQ)
