@@ -186,6 +186,11 @@ int moe_head_argmax(moe_head* h, int T, const uint16_t* x, int rule, int32_t* id
 /* The same on device pointers, enqueued on the head's stream and not synchronised. */
 int moe_head_argmax_dev(moe_head* h, int T, const uint16_t* x, int rule, int32_t* ids, float* best, float* logits);
 
+/* Per-layer RMSNorm (input_layernorm / post_attention_layernorm; host.rs:71-76, as the head's final norm above):
+ * out[t] = bf16(bf16(x[t] * r) * w), r = 1 / sqrt(sum(x[t]^2) / H + eps).  x, out [T, H] bf16, w [H] bf16; device
+ * pointers, enqueued on `stream` (NULL: the null stream).  Returns MOE_GPU_EINVAL / MOE_GPU_EHIP without a message. */
+int moe_rmsnorm_dev(int T, int H, const uint16_t* x, const uint16_t* w, float eps, uint16_t* out, void* stream);
+
 /* ----------------------------------------------------------------------------------------------- decode attention
  * GQA attention of one token over a layer's KV cache, replacing the host step's core (track2_opt/solar_engine/src/
  * main.rs:86-104): for q head h and kv head h / (NQ / NKV), positions t < S,

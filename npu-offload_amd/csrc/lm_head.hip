@@ -190,6 +190,27 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
     }
 }
 
+// One workgroup per token row: the per-layer RMSNorm of host.rs:71-76 (input_layernorm / post_attention_layernorm),
+// the same arithmetic as the head's prologue.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out, int H,
+                                                      float eps) {
+    __shared__ float red[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint16_t* xt = x + (size_t)blockIdx.x * H;
+    float s = 0.f;
+    for (int i = tid; i < H; i += 256) {
+        const float v = bf2f(xt[i]);
+        s = fmaf(v, v, s);
+    }
+    s = wave_sum(s);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    const float ms = (red[0] + red[1] + red[2] + red[3]) / (float)H;
+    const float r = 1.0f / sqrtf(ms + eps);
+    for (int i = tid; i < H; i += 256)
+        out[(size_t)blockIdx.x * H + i] = (uint16_t)f2bf(bf2f(f2bf(bf2f(xt[i]) * r)) * bf2f(w[i]));
+}
+
 }  // namespace
 
 struct moe_head {
@@ -405,6 +426,14 @@ int moe_head_argmax(moe_head* h, int T, const uint16_t* x, int rule, int32_t* id
         HCHK(h, hipMemcpyAsync(logits, h->d_logits, (size_t)T * h->V * sizeof(float), hipMemcpyDeviceToHost,
                                h->stream));
     HCHK(h, hipStreamSynchronize(h->stream));
+    return MOE_GPU_OK;
+}
+
+int moe_rmsnorm_dev(int T, int H, const uint16_t* x, const uint16_t* w, float eps, uint16_t* out, void* stream) {
+    if (T < 1 || H < 1 || H > (1 << 20) || !x || !w || !out || !(eps >= 0.f)) return MOE_GPU_EINVAL;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, static_cast<hipStream_t>(stream), x, w, out, H, eps);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
     return MOE_GPU_OK;
 }
 

@@ -38,7 +38,7 @@ SYMBOLS = (
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
-    "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
+    "moe_rmsnorm_dev", "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
 )
 ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
@@ -121,6 +121,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_head_load_dev": (i, [vp, vp, vp]),
         "moe_head_argmax": (i, [vp, i, vp, i, vp, vp, vp]),
         "moe_head_argmax_dev": (i, [vp, i, vp, i, vp, vp, vp]),
+        "moe_rmsnorm_dev": (i, [i, i, vp, vp, f, vp, vp]),
         "moe_attn_workspace_bytes": (C.c_size_t, [i, i, i]),
         "moe_attn_decode_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, C.c_size_t, vp]),
         "moe_attn_last_error": (C.c_char_p, []),
@@ -413,6 +414,15 @@ class LmHead:
     def argmax_dev(self, T: int, x, ids, best, logits=None, rule: int = ARGMAX_FP32):
         """Device pointers; enqueued on the head's stream, not synchronised."""
         self._chk(self.L.moe_head_argmax_dev(self.h, T, _p(x), rule, _p(ids), _p(best), _p(logits)))
+
+
+def rmsnorm_dev(x, w, out, eps: float = 1e-5, stream=None) -> None:
+    """Per-layer RMSNorm (host.rs:71-76) on device tensors: x, out [T, H] and w [H], bf16 bits."""
+    T, H = x.shape
+    assert tuple(out.shape) == (T, H) and tuple(w.shape) == (H,)
+    rc = load_library().moe_rmsnorm_dev(T, H, _p(x), _p(w), eps, _p(out), getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, f"moe_rmsnorm_dev(T={T}, H={H}) failed")
 
 
 def attn_decode_dev(q, k_cache, v_cache, out, workspace, n_q_heads: int, n_kv_heads: int, S: int,

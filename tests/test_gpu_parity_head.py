@@ -169,3 +169,33 @@ def test_solar_head_full_size_and_device_path():
             np.testing.assert_array_equal(bd.cpu().numpy().view(np.uint32), best.view(np.uint32))
     finally:
         head.close()
+
+
+@pytest.mark.parametrize("T,H", [(1, 4096), (5, 4096), (3, 1000)])
+def test_per_layer_rmsnorm(T, H):
+    """moe_rmsnorm_dev against the oracle's rmsnorm (host.rs:71-76).  With x in multiples of 1/4 up to 4 the sum of
+    squares is exact in any order, so the outputs are bit-identical; with random x the GPU's tree sum may move a few
+    elements by one bf16 ulp."""
+    import torch
+
+    from moe_gpu import rmsnorm_dev
+
+    say(f"rmsnorm T={T} H={H}")
+    rng = np.random.default_rng(T * H)
+    w = bf16_normal(rng, H, 0.1, 1.0)
+    x_exact = O.f2bf((rng.integers(-16, 17, size=(T, H)) / 4.0).astype(np.float32))
+    x_rand = bf16_normal(rng, (T, H), 3.0)
+    wd = torch.from_numpy(w.view(np.int16)).to("cuda:0")
+    for x, exact in ((x_exact, True), (x_rand, False)):
+        xd = torch.from_numpy(x.view(np.int16)).to("cuda:0")
+        od = torch.zeros_like(xd)
+        torch.cuda.synchronize()
+        rmsnorm_dev(xd, wd, od)
+        torch.cuda.synchronize()
+        got = od.cpu().numpy().view(np.uint16)
+        ref = np.stack([O.rmsnorm(x[t], w) for t in range(T)])
+        if exact:
+            np.testing.assert_array_equal(got, ref)
+        else:
+            ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+            assert ulps.max() <= 1 and (ulps > 0).mean() <= 1e-2
