@@ -302,7 +302,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the expert tier would shard by expert "
+        print("bench.py measures one GPU: this library has no multi-GPU path (the expert tier would shard by expert "
               "across GPUs, which is designed but not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 /*
  * moe_oracle.c — CPU restatement of npu-offload's routed-MoE data plane.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/, the smoke check and the CPU-baseline leg of
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle: only tests/, the smoke check and the CPU-baseline leg of
  * the benchmark load it.  The GPU product path never calls into it (libmoe_gpu.so does not link it and fails loudly
  * when its own HIP kernels are missing).
  *

@@ -1,4 +1,4 @@
-"""Python front-end of the CPU oracle (TEST INFRASTRUCTURE — the checker, never the product).
+"""Python front-end of the CPU oracle (TEST INFRASTRUCTURE: it checks the product, it is never the product).
 
 Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` import this module.  It wraps
 three libraries built by ``oracle/Makefile``:
