@@ -191,6 +191,16 @@ int moe_head_argmax_dev(moe_head* h, int T, const uint16_t* x, int rule, int32_t
  * pointers, enqueued on `stream` (NULL: the null stream).  Returns MOE_GPU_EINVAL / MOE_GPU_EHIP without a message. */
 int moe_rmsnorm_dev(int T, int H, const uint16_t* x, const uint16_t* w, float eps, uint16_t* out, void* stream);
 
+/* Projection GEMV of one token with the host's rounding (main.rs:109-111, :119: gemv then round_bf): y[m] = bf16(sum_k
+ * W[m,k] x[k]) (fp32 accumulation in the GPU's order).  W [M, K] bf16 row-major, x [K], y [M]; K % 1024 == 0,
+ * K <= 65536, W and x 16-byte aligned.  Device pointers, enqueued on `stream`. */
+int moe_gemv_dev(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y, void* stream);
+/* Rotary embedding in place (main.rs:65-77, HF rotate_half in bf16): for each of n_heads rows of head_dim,
+ * x[i] = bf16(bf16(x[i] * cos[i]) + bf16(rot[i] * sin[i])), rot = (-x[D/2..D), x[0..D/2)).  cos_row / sin_row: the
+ * bf16 [head_dim] rows of the position (rope_cos.bin / rope_sin.bin).  head_dim even, <= 1024. */
+int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row, const uint16_t* sin_row,
+                 void* stream);
+
 /* ----------------------------------------------------------------------------------------------- decode attention
  * GQA attention of one token over a layer's KV cache, replacing the host step's core (track2_opt/solar_engine/src/
  * main.rs:86-104): for q head h and kv head h / (NQ / NKV), positions t < S,

@@ -38,7 +38,8 @@ SYMBOLS = (
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
-    "moe_rmsnorm_dev", "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
+    "moe_rmsnorm_dev", "moe_gemv_dev", "moe_rope_dev", "moe_attn_workspace_bytes", "moe_attn_decode_dev",
+    "moe_attn_last_error",
 )
 ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
@@ -122,6 +123,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_head_argmax": (i, [vp, i, vp, i, vp, vp, vp]),
         "moe_head_argmax_dev": (i, [vp, i, vp, i, vp, vp, vp]),
         "moe_rmsnorm_dev": (i, [i, i, vp, vp, f, vp, vp]),
+        "moe_gemv_dev": (i, [i, i, vp, vp, vp, vp]),
+        "moe_rope_dev": (i, [i, i, vp, vp, vp, vp]),
         "moe_attn_workspace_bytes": (C.c_size_t, [i, i, i]),
         "moe_attn_decode_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, C.c_size_t, vp]),
         "moe_attn_last_error": (C.c_char_p, []),
@@ -423,6 +426,22 @@ def rmsnorm_dev(x, w, out, eps: float = 1e-5, stream=None) -> None:
     rc = load_library().moe_rmsnorm_dev(T, H, _p(x), _p(w), eps, _p(out), getattr(stream, "cuda_stream", stream))
     if rc != OK:
         raise MoeGpuError(rc, f"moe_rmsnorm_dev(T={T}, H={H}) failed")
+
+
+def gemv_dev(W, x, y, stream=None) -> None:
+    """Projection GEMV with round_bf (main.rs:109-111): W [M, K], x [K], y [M], bf16 bits on the device."""
+    M, K = W.shape
+    rc = load_library().moe_gemv_dev(M, K, _p(W), _p(x), _p(y), getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, f"moe_gemv_dev(M={M}, K={K}) failed")
+
+
+def rope_dev(x, cos_row, sin_row, stream=None) -> None:
+    """Rotary embedding in place (main.rs:65-77): x [n_heads, D] bf16 bits on the device, cos/sin rows [D]."""
+    n, D = x.shape
+    rc = load_library().moe_rope_dev(n, D, _p(x), _p(cos_row), _p(sin_row), getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, f"moe_rope_dev(n={n}, D={D}) failed")
 
 
 def attn_decode_dev(q, k_cache, v_cache, out, workspace, n_q_heads: int, n_kv_heads: int, S: int,

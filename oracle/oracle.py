@@ -12,7 +12,7 @@ three libraries built by ``oracle/Makefile``:
 Function names follow the reference: ``cpu_moe`` (cpu_moe.cpp:38), ``ck_moe3`` (cpu_kern.c:141), ``gemv``
 (cpu_kern.c:32), ``quant_row``/``quant_expert`` (cpu_kern.c:218, :227), ``moe_q8w`` (cpu_kern.c:306), ``route``
 (host.rs.tpl:247), ``group_tokens`` (runtime.py:344-347), ``rmsnorm`` (host.rs:71-76), ``lm_head_argmax``
-(main.rs:384-385, chip.rs:183-194), ``attention`` (main.rs:86-104).
+(main.rs:384-385, chip.rs:183-194), ``attention`` (main.rs:86-104), ``rope`` (main.rs:65-77).
 """
 from __future__ import annotations
 
@@ -195,6 +195,17 @@ def lm_head_argmax(logits: np.ndarray, rule: int = 0):
         v = bf2f(f2bf(v))
     i = int(np.argmax(v))
     return i, float(v[i])
+
+
+def rope(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
+    """main.rs:65-77 for one position: x bf16 bits [n_heads, D]; rot = (-x[D/2:], x[:D/2]);
+    out = bf16(bf16(x * cos) + bf16(rot * sin)), every product and sum in fp32."""
+    xf = bf2f(np.ascontiguousarray(x, np.uint16))
+    D = xf.shape[-1]
+    rot = np.concatenate([-xf[..., D // 2:], xf[..., :D // 2]], axis=-1)
+    a = bf2f(f2bf(xf * bf2f(cos_row)))
+    b = bf2f(f2bf(rot * bf2f(sin_row)))
+    return f2bf(a + b).reshape(x.shape)
 
 
 def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_kv: int, scale: float | None = None):

@@ -412,3 +412,24 @@ def test_attention_equal_keys_give_uniform_weights():
     assert np.all(sc == sc[:, :1])
     ref = O.bf2f(v).astype(np.float64)[:, 0, :].mean(axis=0)  # p = bf16(1/64) = 1/64 exactly
     assert np.max(np.abs(O.bf2f(out[0]) - ref)) <= 2.0 ** -8 * np.max(np.abs(ref)) + 1e-6
+
+
+def test_rope_hand_values_and_rotation():
+    # D = 4, cos = 1, sin = 0: identity; cos = 0, sin = 1: x -> rotate_half(x) = (-x2, -x3, x0, x1)
+    x = O.f2bf(np.array([[1.0, 2.0, 3.0, 4.0]], np.float32))
+    one, zero = O.f2bf(np.ones(4, np.float32)), O.f2bf(np.zeros(4, np.float32))
+    assert np.array_equal(O.rope(x, one, zero), x)
+    assert O.bf2f(O.rope(x, zero, one)).tolist() == [[-3.0, -4.0, 1.0, 2.0]]
+    # an angle: cos = sin = 0.5 (exact in bf16): out = bf16(0.5 x + 0.5 rot)
+    half = O.f2bf(np.full(4, 0.5, np.float32))
+    assert O.bf2f(O.rope(x, half, half)).tolist() == [[-1.0, -1.0, 2.0, 3.0]]
+    # against float64 rotation within the three bf16 roundings
+    rng = np.random.default_rng(11)
+    D = 128
+    xr = O.f2bf(rng.standard_normal((8, D)).astype(np.float32))
+    th = rng.uniform(0, 2 * np.pi, D // 2)
+    c = O.f2bf(np.cos(np.concatenate([th, th])).astype(np.float32))
+    s = O.f2bf(np.sin(np.concatenate([th, th])).astype(np.float32))
+    xf = O.bf2f(xr).astype(np.float64)
+    ref = xf * O.bf2f(c) + np.concatenate([-xf[:, D // 2:], xf[:, :D // 2]], axis=1) * O.bf2f(s)
+    assert np.max(np.abs(O.bf2f(O.rope(xr, c, s)) - ref)) <= 3 * 2.0 ** -8 * np.max(np.abs(xf)) + 1e-6
