@@ -274,6 +274,66 @@ def bench_attn(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_proj(args) -> None:
+    """The attention block's projections of one token (q 4096 x 4096, k and v 1024 x 4096, o 4096 x 4096: 83.9 MB of
+    bf16 weights per layer, main.rs:109-111 and :119), rotating over 8 layers (671 MB)."""
+    import torch
+
+    from moe_gpu import gemv_dev
+
+    H, QD, KVD, L, K, W_ = 4096, 4096, 1024, 8, args.steps, args.warmup
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    g = torch.Generator(device=dev).manual_seed(0)
+    log(f"proj: {L} layers of q/k/v/o weights")
+    # q, k and v read the same input: the engine places them as one [QD + 2 KVD, H] table, one launch
+    fused = not args.proj_separate
+    shapes = [(QD + 2 * KVD, H), (H, QD)] if fused else [(QD, H), (KVD, H), (KVD, H), (H, QD)]
+    ws = [[(torch.randn(m, k, device=dev, generator=g) * 0.02).to(torch.bfloat16).view(torch.int16) for m, k in shapes]
+          for _ in range(L)]
+    h = torch.randn(H, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    a_in = torch.randn(QD, device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    outs = [torch.zeros(m, dtype=torch.int16, device=dev) for m, _ in shapes]
+    torch.cuda.synchronize()
+
+    def step(i):
+        wl = ws[i % L]
+        for j in range(len(shapes) - 1):
+            gemv_dev(wl[j], h, outs[j], stream=stream)
+        gemv_dev(wl[-1], a_in, outs[-1], stream=stream)
+
+    for i in range(W_):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_us = e0.elapsed_time(e1) / K * 1e3
+    nbytes = sum(m * k for m, k in shapes) * 2
+    achieved = nbytes / (ev_us * 1e-6) / 1e9
+    line = {
+        "metric": "attention-block projections (q/k/v/o GEMV, H=4096, 32 q / 8 kv heads) µs/layer/token + achieved "
+                  "HBM TB/s, bf16 batch 1",
+        "value": round(wall_ms * 1e3 / K, 2), "unit": "us/layer/token", "n_gpus": 1, "steps": K, "warmup": W_,
+        "ms_per_step": round(wall_ms / K, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded, weights ~N(0,0.02))", "event_ms_per_step": round(ev_us / 1e3, 5),
+        "config": {"workload": "proj: q/k/v/o projections of one token, H=4096, QD=4096, KVD=1024, bf16", "tokens": 1,
+                   "qkv_one_table": fused},
+        "roofline": {"kernel": f"gemv_kernel x {len(shapes)}", "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes, "avg_us": round(ev_us, 2),
+                     "timing": "timed-region hipEvents over the GEMV launches of a step"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` on bench workload `workload` from the committed rocprofv3 counter summary
     (profiles/<kernel>_<workload>_traffic.txt, line `traffic_bytes_per_launch: N`), or None."""
@@ -293,9 +353,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head", "attn"])
+    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head", "attn", "proj"])
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--proj-separate", action="store_true", help="proj workload: q, k, v as three launches")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run 5 plain device copies of MIB MiB (reference kernel for rocprof "
@@ -311,6 +372,9 @@ def main():
         return
     if args.workload == "attn":
         bench_attn(args)
+        return
+    if args.workload == "proj":
+        bench_proj(args)
         return
 
     import torch

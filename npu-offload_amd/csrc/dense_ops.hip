@@ -133,7 +133,10 @@ int moe_gemv_dev(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y
     if (M < 1 || K < 1024 || K % 1024 != 0 || K > 65536 || !W || !x || !y) return MOE_GPU_EINVAL;
     if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15) return MOE_GPU_EINVAL;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    return K % 4096 == 0 ? gemv_launch<4, 8>(W, x, y, M, K, st) : gemv_launch<8, 2>(W, x, y, M, K, st);
+    // whole 4096-column rows when K allows; 4 rows per wave step for tall W, 1 row for short W (1024 rows x 4 is a
+    // quarter of the waves the chip holds)
+    if (K % 4096 == 0) return M >= 4096 ? gemv_launch<4, 8>(W, x, y, M, K, st) : gemv_launch<1, 8>(W, x, y, M, K, st);
+    return gemv_launch<8, 2>(W, x, y, M, K, st);
 }
 
 int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row, const uint16_t* sin_row,
