@@ -101,14 +101,33 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* x, const uint16_t* 
     }
 }
 
+// Resident workgroups per (device, kernel, LDS size), queried once per thread: a launch stays one host call.
 int gemv_grid(const void* fn, size_t lds, int M, int RB, int* grid) {
-    int dev = 0, ncu = 0, per_cu = 0;
+    struct Entry {
+        int dev;
+        const void* fn;
+        size_t lds;
+        int wgs;
+    };
+    static thread_local Entry cache[8];
+    static thread_local int n_cache = 0;
+    int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return MOE_GPU_EHIP;
-    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MOE_GPU_EHIP;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) return MOE_GPU_EHIP;
-    if (per_cu < 1) return MOE_GPU_EINVAL;
+    int wgs = 0;
+    for (int i = 0; i < n_cache; ++i)
+        if (cache[i].dev == dev && cache[i].fn == fn && cache[i].lds == lds) wgs = cache[i].wgs;
+    if (wgs == 0) {
+        int ncu = 0, per_cu = 0;
+        if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return MOE_GPU_EHIP;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MOE_GPU_EHIP;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) return MOE_GPU_EHIP;
+        if (per_cu < 1) return MOE_GPU_EINVAL;
+        wgs = ncu * per_cu;
+        cache[n_cache < 8 ? n_cache++ : 7] = Entry{dev, fn, lds, wgs};
+    }
     const int need = ((M + RB - 1) / RB + kWaves - 1) / kWaves;
-    *grid = ncu * per_cu < need ? ncu * per_cu : need;
+    *grid = wgs < need ? wgs : need;
     return MOE_GPU_OK;
 }
 
@@ -116,8 +135,6 @@ template <int RB, int CG>
 int gemv_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, int M, int K, hipStream_t st) {
     const void* fn = reinterpret_cast<const void*>(&gemv_kernel<RB, CG>);
     const size_t lds = (size_t)K * sizeof(uint16_t);
-    if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-        return MOE_GPU_EHIP;
     int grid = 0, rc = gemv_grid(fn, lds, M, RB, &grid);
     if (rc != MOE_GPU_OK) return rc;
     hipLaunchKernelGGL((gemv_kernel<RB, CG>), dim3(grid), dim3(256), lds, st, W, x, y, M, K);
