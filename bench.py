@@ -334,6 +334,158 @@ def bench_proj(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+DEC_NQ, DEC_NKV, DEC_D, DEC_CTX, DEC_L, DEC_V = 32, 8, 128, 4096, 48, 196608
+DECODE_METRIC = ("decode tokens/s, 48-layer Solar-scale MoE decoder (GQA 32 q / 8 kv heads, KV 4096, 128+1 experts "
+                 "top-8, LM head 196608), bf16 batch 1")
+
+
+def rope_rows(max_ctx: int, D: int = 128, theta: float = 1e6):
+    """cos / sin [max_ctx, D] bf16 bits, HF layout (the frequencies repeated for both halves)."""
+    inv = theta ** (-np.arange(0, D, 2, dtype=np.float64) / D)
+    ang = np.arange(max_ctx, dtype=np.float64)[:, None] * inv[None, :]
+    ang = np.concatenate([ang, ang], axis=1).astype(np.float32)
+    f = lambda a: ((a.view(np.uint32).astype(np.uint64) + 0x7FFF + ((a.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    return f(np.cos(ang)), f(np.sin(ang))
+
+
+def cpu_baseline_decode(budget_layers: int = 2) -> dict | None:
+    """The reference host step's arithmetic for `budget_layers` layers on this host's cores, scaled to 48 layers + the
+    LM head: the reference's own ck_gemv for the q|k|v, o, router and LM-head GEMVs and ck_moe3 for the 9 experts
+    (cpu_kern.c, built from its source), the oracle's numpy restatement of the attention (main.rs:86-104; the Rust
+    host attention cannot be built here)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    if not O.ref_available():
+        return None
+    H, F, E, QD, KVD = 4096, 1280, 128, DEC_NQ * DEC_D, DEC_NKV * DEC_D
+    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    R = O.Ref()
+    R.set_threads(cores)
+    rng = np.random.default_rng(0)
+    bf = lambda shape, sd: O.f2bf((sd * rng.standard_normal(shape)).astype(np.float32))
+    wqkv, wo, wr = bf((QD + 2 * KVD, H), 0.02), bf((H, QD), 0.02), bf((E, H), 0.02)
+    kc, vc = bf((DEC_CTX, DEC_NKV, DEC_D), 1.0), bf((DEC_CTX, DEC_NKV, DEC_D), 1.0)
+    n = F * H
+    src = O.f2bf((np.arange(3 * n) % 97).astype(np.float32) * 1e-4)
+    g, u, d = src[:n].reshape(F, H), src[n:2 * n].reshape(F, H), src[2 * n:].reshape(H, F)
+    pool = [R.place_expert(g, u, d) for _ in range(18)]
+    wln = np.ones(H, np.uint16) * 0x3F80
+    x = bf(H, 1.0)
+    t0 = time.perf_counter()
+    for l in range(budget_layers):
+        h = O.rmsnorm(x, wln)
+        qkv = O.f2bf(R.gemv(wqkv, h))
+        a, _ = O.attention(qkv[:QD].reshape(DEC_NQ, DEC_D), kc, vc, DEC_NKV)
+        o = O.f2bf(R.gemv(wo, a.ravel()))
+        h2 = O.rmsnorm(O.f2bf(O.bf2f(x) + O.bf2f(o)), wln)
+        lg = R.gemv(wr, h2)
+        ids, gates = O.route(lg[None], None, 8)
+        out = np.zeros(H, np.float32)
+        R.moe3(pool[9 * (l % 2):9 * (l % 2) + 1], np.ones(1, np.float32), h2, out, H, F)
+        R.moe3(pool[9 * (l % 2) + 1:9 * (l % 2) + 9], gates[0], h2, out, H, F)
+        x = O.f2bf(O.bf2f(x) + out)
+    per_layer = (time.perf_counter() - t0) / budget_layers
+    # the LM head: ck_gemv over a 1/8 slice of the table, scaled
+    W = np.tile(bf((64, H), 0.02), (DEC_V // 8 // 64, 1))
+    t1 = time.perf_counter()
+    R.gemv(W, x)
+    head = (time.perf_counter() - t1) * 8
+    tok_s = 1.0 / (DEC_L * per_layer + head)
+    return {"value": round(tok_s, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{budget_layers} decode layers (rmsnorm + cpu_kern.c ck_gemv q|k|v/o/router + numpy attention over "
+                      f"4096 positions + ck_moe3 shared + 8 routed experts) and 1/8 of the LM-head ck_gemv, scaled to "
+                      f"48 layers + the full head; {per_layer * 1e3:.1f} ms per layer, {head * 1e3:.1f} ms head"}
+
+
+def bench_decode(args) -> None:
+    """Greedy decode steps of a 48-layer Solar-scale MoE decoder with every weight resident (about 203 GB): per layer
+    RMSNorm + q|k|v GEMV, RoPE + KV append, GQA attention over 4096 positions, o GEMV, the Solar MoE block (softmax
+    top-8 with the Zipf-skewed router bias of the Solar layer workload), then the final norm, the 196608-row LM head
+    and the argmax.  Each step attends over 4096 positions (the step's own row at position 4095 included); steps
+    chain on the device (a step's token is the previous step's pick)."""
+    import torch
+
+    from moe_gpu import ROUTE_SOFTMAX, MoeModel
+
+    H, F, E, k, S, L, V = 4096, 1280, 128, 8, 1, DEC_L, DEC_V
+    QD, KVD = DEC_NQ * DEC_D, DEC_NKV * DEC_D
+    K, W_ = args.steps, args.warmup
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    log(f"decode: create a {L}-layer model")
+    m = MoeModel(H, DEC_NQ, DEC_NKV, F, E, k, S, L, V, DEC_CTX, route_rule=ROUTE_SOFTMAX)
+    m.set_stream(stream)
+    tier = m.experts
+    c02 = synth_c(0.02)
+    kv_key = lambda l, j: synth_key(9, (1 << 41) + 2 * l + j)
+    buf = torch.empty((QD + 2 * KVD) * H + H * QD + 2 * H, dtype=torch.int16, device=dev)
+    for l in range(L):
+        tier.synth_layer(l, 2000 + l, 0.02, zipf_bias(E, 1.1, 2000 + l))
+        tier.synth_fill(buf, buf.numel(), synth_key(11, (1 << 42) + l), c02)
+        o0, o1, o2, o3 = QD * H, (QD + KVD) * H, (QD + 2 * KVD) * H, (QD + 2 * KVD) * H + H * QD
+        norm = torch.full((H,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
+        m.load_layer(l, norm, buf[:o0], buf[o0:o1], buf[o1:o2], buf[o2:o3], norm)
+        kd, vd = m.kv_cache(l)
+        for j, p in enumerate((kd, vd)):
+            tier.synth_fill(p, (DEC_CTX - 1) * KVD, kv_key(l, j), synth_c(1.0))
+        if l % 8 == 7:
+            log(f"  {l + 1} layers resident")
+    del buf
+    emb = torch.empty((V, H), dtype=torch.int16, device=dev)
+    tier.synth_fill(emb, V * H, synth_key(12, 1 << 43), synth_c(1.0))
+    m.load_embedding(emb)
+    tier.synth_fill(emb, V * H, synth_key(13, 1 << 43), c02)
+    m.head.load_dev(emb, torch.full((H,), 0x3F80, dtype=torch.int16, device=dev))
+    del emb
+    torch.cuda.empty_cache()
+    cs, sn = rope_rows(DEC_CTX)
+    m.load_rope(cs, sn)
+    toks = torch.zeros(K + W_ + 1, dtype=torch.int32, device=dev)
+    toks[0] = 1
+    best = torch.zeros(1, dtype=torch.float32, device=dev)
+    pos = DEC_CTX - 1
+    torch.cuda.synchronize()
+    log(f"warmup {W_} steps")
+    for i in range(W_):
+        m.step_dev(toks[i:i + 1], pos, toks[i + 1:i + 2], best)
+    m.synchronize()
+    log(f"timing {K} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(W_, W_ + K):
+        m.step_dev(toks[i:i + 1], pos, toks[i + 1:i + 2], best)
+    e1.record(stream)
+    m.synchronize()
+    wall_s = time.perf_counter() - t0
+    ev_s = e0.elapsed_time(e1) / 1e3
+    ms_tok = wall_s / K * 1e3
+    # algorithmic bytes per token: every weight byte once (attention block, router, shared + routed experts, LM head)
+    # and the KV rows read; the distinct routed experts of a token are 8 at batch 1
+    per_layer = (QD + 2 * KVD) * H * 2 + H * QD * 2 + 2 * DEC_CTX * KVD * 2 + E * H * 2 + (k + S) * 3 * F * H * 2
+    nbytes = L * per_layer + V * H * 2 + H * 2
+    achieved = nbytes / (ev_s / K) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
+    line = {
+        "metric": DECODE_METRIC, "value": round(K / wall_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+        "warmup": W_, "ms_per_step": round(ms_tok, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded device generator; weights ~0.02 sd, "
+        "embeddings and KV ~1 sd, norm weights 1)", "event_ms_per_step": round(ev_s / K * 1e3, 4),
+        "config": {"workload": "decode: 48 layers x (RMSNorm + GQA attention 32q/8kv d128 over KV 4096 + RMSNorm + "
+                               "Solar MoE block H4096 F1280 E128+1 top-8) + LM head V196608, greedy, batch 1",
+                   "layers": L, "kv_len": DEC_CTX, "vocab": V, "tokens": 1},
+        "roofline": {"kernel": "whole step (7 launches per layer + head)", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": int(nbytes), "avg_us": round(ev_s / K * 1e6, 1),
+                     "timing": "timed-region hipEvents on the model's stream over K chained steps"},
+        "cpu_baseline": cpu,
+    }
+    m.close()
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` on bench workload `workload` from the committed rocprofv3 counter summary
     (profiles/<kernel>_<workload>_traffic.txt, line `traffic_bytes_per_launch: N`), or None."""
@@ -353,7 +505,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head", "attn", "proj"])
+    ap.add_argument("--workload", default="solar", choices=sorted(WORKLOADS) + ["lm-head", "attn", "proj", "decode"])
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers the steps rotate over")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--proj-separate", action="store_true", help="proj workload: q, k, v as three launches")
@@ -375,6 +527,9 @@ def main():
         return
     if args.workload == "proj":
         bench_proj(args)
+        return
+    if args.workload == "decode":
+        bench_decode(args)
         return
 
     import torch

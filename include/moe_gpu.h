@@ -18,9 +18,14 @@
  * Expert math (solar_hybrid/cpu_moe.cpp:38-96 semantics): for expert e and token t,
  *   g = Wg_e x_t, u = Wu_e x_t (fp32 accumulation of bf16 products), act = bf16(silu(g) * u),
  *   y_e[t] = Wd_e act (fp32).
- * Routing (npu-kernels/.../layer_template/src/host.rs.tpl:247-267, softmax scoring): score = logits + bias; the k
- * largest scores are selected (exact ties -> lower expert index); gates over the first `keep` ranks are the
- * softmax restricted to them (renormalised); ranks >= keep are dropped (their gate is 0).
+ * Router logits: logits[t, e] = W_r[e] . x[t] in the reference's own summation order (ck_gemv, cpu_kern.c:9-19,
+ * :31-35): bit-identical to it whenever no product or partial sum is a denormal fp32 number.
+ * Routing, by the context's MOE_GPU_OPT_ROUTE_RULE (ties in the selection always go to the lower expert index):
+ *   MOE_GPU_ROUTE_SOFTMAX (default; npu-kernels/.../layer_template/src/host.rs.tpl:247-267): score = logits + bias;
+ *     the k largest scores are selected; gates over the first `keep` ranks are the softmax restricted to them
+ *     (renormalised); ranks >= keep are dropped (their gate is 0).
+ *   MOE_GPU_ROUTE_SIGMOID (Solar's route(), track2_opt/solar_engine/src/host.rs:119-128): s = 1 / (1 + exp(-logit)),
+ *     selection by s + bias (the bias only selects), gates s_r / (sum_{q < keep} s_q + 1e-20).
  * Combine, per token, in this fixed order: out[t] (= 0, or the caller's value with MOE_GPU_ACCUMULATE)
  *   += y_shared_s[t] for s = 0..S-1, then += gate[t,r] * y_{id[t,r]}[t] for r = 0..keep-1 (one fused multiply-add
  *   per term).  A token's result does not depend on which other tokens share the call.
@@ -52,7 +57,11 @@ enum {
 
 /* ----------------------------------------------------------------------------------------------- context
  * Replaces Chip::spawn (track2_opt/solar_engine/src/chip.rs:96-111) for a HIP device: creates the stream and the
- * per-call workspace.  Layer tables are allocated on first load.  n_layers bounds the layer index. */
+ * per-call workspace.  Layer tables are allocated on first load, each kind on its own (router, bf16 routed experts,
+ * shared experts, int8 routed experts): a layer whose routed experts are only loaded as int8 holds no bf16 routed
+ * tables.  n_layers bounds the layer index.
+ * The layer / moe calls refuse a stream that is capturing a graph (MOE_GPU_ESTATE): their epochs and work queue are
+ * per launch, so a replayed launch would read the previous replay's words. */
 int moe_gpu_create(int device, int H, int F, int E, int topk, int n_shared, int n_layers, int max_tokens,
                    moe_gpu** out);
 void moe_gpu_destroy(moe_gpu* ctx);
@@ -109,9 +118,20 @@ int moe_gpu_layer(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, u
  * Same operations on device pointers, enqueued on the context's stream without synchronising. */
 int moe_gpu_route_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, int32_t* ids, float* gates,
                       float* logits);
+/* moe_dev cannot check device-side ids, so it requires every routed expert of the layer to be loaded in the call's
+ * precision (with MOE_GPU_INT8: a current int8 copy of each; a bf16 reload makes an expert's int8 copy stale). */
 int moe_gpu_moe_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates,
                     int keep, int with_shared, unsigned flags, float* out);
 int moe_gpu_layer_dev(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, unsigned flags, float* out,
+                      int32_t* ids, float* gates);
+/* A decode layer's second half as one call (track2_opt/solar_engine/src/main.rs:120-141, the residual add, the
+ * post-attention RMSNorm and moe_host): with r = bf16(resid + attn_o) and h2 = rmsnorm(r, norm_w) (host.rs:71-76;
+ * the sum of squares in the GPU's fixed order), the layer call on h2 (routing by the context's rule), then
+ *   x_next = bf16(r + bf16(bf16(routed) + bf16(shared)))   (the routed and shared sums as moe_host rounds them).
+ * resid, attn_o, x_next [T, H] bf16, norm_w [H] bf16; out [T, H] fp32 (the layer output, optional), ids / gates
+ * optional.  MOE_GPU_ACCUMULATE is not accepted.  Device pointers, enqueued, not synchronised. */
+int moe_gpu_block_dev(moe_gpu* ctx, int layer, int T, const uint16_t* resid, const uint16_t* attn_o,
+                      const uint16_t* norm_w, float eps, int keep, unsigned flags, uint16_t* x_next, float* out,
                       int32_t* ids, float* gates);
 
 /* ----------------------------------------------------------------------------------------------- bench/test support
@@ -134,7 +154,13 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
  * part); it changes the summation order, identically in both paths.  MOE_GPU_OPT_KSPLIT_SHARED: the same for the shared
  * experts' tiles (0 = automatic, the same rule).  MOE_GPU_OPT_LAG: fused queue order, a routed slot's down
  * tiles are queued after the gate|up parts of the routed slot `lag` places later (0 = automatic).  MOE_GPU_OPT_SHARED_WAITS: 1
- * holds the shared experts' gate|up parts until the routing is known (0 = stream them while routing). */
+ * holds the shared experts' gate|up parts until the routing is known (0 = stream them while routing).
+ * MOE_GPU_OPT_GRID: fused grid size in workgroups (0 = automatic: what fits at once); a larger grid is allowed (units
+ * are handed out by a queue to running workgroups only, so a grid that is not all resident still completes).
+ * MOE_GPU_OPT_ROUTER_POLL: passes of the bounded wait for the router logits (default 1024) after which a workgroup
+ * computes the missing router rows itself (a router unit whose workgroup is not resident then cannot hold the call
+ * up); 0 computes them at the first miss (a test of that path; the bits are the same).  MOE_GPU_OPT_ROUTE_RULE:
+ * MOE_GPU_ROUTE_SOFTMAX (default) or MOE_GPU_ROUTE_SIGMOID, see the routing rules above. */
 #define MOE_GPU_OPT_FUSED 1
 #define MOE_GPU_OPT_WG_PER_CU 2
 #define MOE_GPU_OPT_LAST_GRID 3
@@ -142,6 +168,11 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 #define MOE_GPU_OPT_LAG 5
 #define MOE_GPU_OPT_SHARED_WAITS 6
 #define MOE_GPU_OPT_KSPLIT_SHARED 7
+#define MOE_GPU_OPT_GRID 8
+#define MOE_GPU_OPT_ROUTER_POLL 9
+#define MOE_GPU_OPT_ROUTE_RULE 10
+#define MOE_GPU_ROUTE_SOFTMAX 0
+#define MOE_GPU_ROUTE_SIGMOID 1
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
@@ -195,11 +226,26 @@ int moe_rmsnorm_dev(int T, int H, const uint16_t* x, const uint16_t* w, float ep
  * W[m,k] x[k]) (fp32 accumulation in the GPU's order).  W [M, K] bf16 row-major, x [K], y [M]; K % 1024 == 0,
  * K <= 65536, W and x 16-byte aligned.  Device pointers, enqueued on `stream`. */
 int moe_gemv_dev(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y, void* stream);
+/* fp32 GEMV in the reference's own order: y[m] = W[m] . x summed exactly as ck_gemv does (cpu_kern.c:9-19, :31-35: two
+ * 16-lane vdpbf16ps accumulators over 64-element steps, then GCC's reduce tree), so y is bit-identical to ck_gemv's
+ * whenever no product or partial sum is a denormal fp32 number.  K % 512 == 0, K <= 65536, W and x 16-byte aligned.
+ * Device pointers, enqueued on `stream`. */
+int moe_gemv_f32_dev(int M, int K, const uint16_t* W, const uint16_t* x, float* y, void* stream);
+/* The same GEMV on rmsnorm(x, norm_w) (host.rs:71-76), which each workgroup computes from the residual x [K] itself:
+ * a layer's input norm folded into its q|k|v projection (main.rs:108-111).  The sum of squares runs in the GPU's fixed
+ * order (per thread over strided elements, a 64-lane butterfly, then the 4 wavefronts in order). */
+int moe_gemv_norm_dev(int M, int K, const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, float eps,
+                      uint16_t* y, void* stream);
 /* Rotary embedding in place (main.rs:65-77, HF rotate_half in bf16): for each of n_heads rows of head_dim,
  * x[i] = bf16(bf16(x[i] * cos[i]) + bf16(rot[i] * sin[i])), rot = (-x[D/2..D), x[0..D/2)).  cos_row / sin_row: the
  * bf16 [head_dim] rows of the position (rope_cos.bin / rope_sin.bin).  head_dim even, <= 1024. */
 int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row, const uint16_t* sin_row,
                  void* stream);
+/* The step between the projection and attention in one launch (main.rs:112-118): qkv = [q (NQ*D) | k (NKV*D) |
+ * v (NKV*D)] bf16; q is roped in place, k is roped into k_cache[pos] and v copied into v_cache[pos] (caches
+ * [max_ctx, NKV, D]).  Device pointers, enqueued on `stream`. */
+int moe_rope_append_dev(int n_q_heads, int n_kv_heads, int head_dim, uint16_t* qkv, const uint16_t* cos_row,
+                        const uint16_t* sin_row, uint16_t* k_cache, uint16_t* v_cache, int pos, void* stream);
 
 /* ----------------------------------------------------------------------------------------------- decode attention
  * GQA attention of one token over a layer's KV cache, replacing the host step's core (track2_opt/solar_engine/src/
@@ -214,6 +260,49 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
                         const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
                         size_t workspace_bytes, void* stream);
 const char* moe_attn_last_error(void); /* message of this thread's last failed moe_attn_decode_dev */
+
+/* ----------------------------------------------------------------------------------------------- decode step
+ * One greedy decode step of a whole MoE decoder, replacing the engine's host step (track2_opt/solar_engine/src/
+ * main.rs:372-387 `step`, with `layer` :106-126 and `moe_host` :128-141): x = embedding[token]; per layer the
+ * input RMSNorm + q|k|v GEMV, RoPE + KV append at pos, GQA attention over positions 0..pos, o GEMV, then
+ * moe_gpu_block_dev (residual add, post-attention RMSNorm, routed + shared experts, residual add); then the final
+ * RMSNorm, the LM head and the greedy argmax.  The model owns a moe_gpu context (its experts and routers: load them
+ * through moe_model_experts()) and a moe_head (moe_model_head()); all run on the model's stream.  Batch 1. */
+typedef struct moe_model moe_model;
+typedef struct moe_model_config {
+    int H, n_q_heads, n_kv_heads, head_dim;  /* head_dim 128; H % 4096 == 0 */
+    int F, E, topk, n_shared;                /* the MoE block (moe_gpu_create) */
+    int n_layers, vocab, max_ctx;            /* max_ctx: KV cache and rope table length */
+    float eps;                               /* RMSNorm epsilon (host.rs:15: 1e-5) */
+    int route_rule;                          /* MOE_GPU_ROUTE_SIGMOID for Solar's route(), or _SOFTMAX */
+    int argmax_rule;                         /* MOE_HEAD_ARGMAX_FP32 (main.rs:384-385) or _BF16 (chip.rs:183-194) */
+} moe_model_config;
+int moe_model_create(int device, const moe_model_config* cfg, moe_model** out);
+void moe_model_destroy(moe_model* m);
+const char* moe_model_last_error(const moe_model* m); /* m == NULL: the last failed create */
+moe_gpu* moe_model_experts(moe_model* m);
+moe_head* moe_model_head(moe_model* m);
+int moe_model_set_stream(moe_model* m, void* stream);
+/* Waits for the model's stream; reports a step whose token id was outside the vocabulary. */
+int moe_model_synchronize(moe_model* m);
+/* Attention-block weights of one layer, host or device pointers, row-major bf16 (model.layers.{l}.*): in_norm [H]
+ * (input_layernorm), wq [NQ*D, H], wk / wv [NKV*D, H], wo [H, NQ*D], post_norm [H] (post_attention_layernorm). */
+int moe_model_load_layer(moe_model* m, int layer, const uint16_t* in_norm, const uint16_t* wq, const uint16_t* wk,
+                         const uint16_t* wv, const uint16_t* wo, const uint16_t* post_norm);
+int moe_model_load_embedding(moe_model* m, const uint16_t* emb);                   /* [vocab, H] bf16 */
+int moe_model_load_rope(moe_model* m, const uint16_t* cos_tab, const uint16_t* sin_tab); /* [max_ctx, D] bf16 */
+/* Steps run the first n layers (default all), then the head: a stage of a model split over several devices, or a
+ * layer-by-layer check. */
+int moe_model_set_layers(moe_model* m, int n);
+/* Device pointers of a layer's KV cache [max_ctx, NKV, D] bf16 (zeroed at create; a caller may fill positions). */
+int moe_model_kv_cache(moe_model* m, int layer, uint16_t** k_cache, uint16_t** v_cache);
+/* token, next: device int32; best (device fp32, optional) receives the picked logit.  Writes the KV caches at pos and
+ * attends over positions 0..pos.  Enqueued, not synchronised. */
+int moe_model_step_dev(moe_model* m, const int32_t* token, int pos, int32_t* next, float* best);
+/* The same from / to host values, synchronous. */
+int moe_model_step(moe_model* m, int token, int pos, int32_t* next, float* best);
+/* The residual stream after the last layer of the last step (before the final norm), [H] bf16 to host or device. */
+int moe_model_residual(moe_model* m, uint16_t* x);
 
 #ifdef __cplusplus
 }

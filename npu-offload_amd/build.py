@@ -14,6 +14,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libmoe_gpu.so")
+CK_LIB = os.path.join(LIBDIR, "libck_gpu.so")  # the reference's cpu_kern.c boundary (ck_*) served by libmoe_gpu
 ARCH = os.environ.get("MOE_GPU_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_fma_f32 & co).
@@ -39,7 +40,8 @@ def _jobs():
     jobs = [(os.path.join(CSRC, "moe_gpu_api.hip"), [], os.path.join(obj, "moe_gpu_api.o")),
             (os.path.join(CSRC, "lm_head.hip"), [], os.path.join(obj, "lm_head.o")),
             (os.path.join(CSRC, "attn_decode.hip"), [], os.path.join(obj, "attn_decode.o")),
-            (os.path.join(CSRC, "dense_ops.hip"), [], os.path.join(obj, "dense_ops.o"))]
+            (os.path.join(CSRC, "dense_ops.hip"), [], os.path.join(obj, "dense_ops.o")),
+            (os.path.join(CSRC, "decode_model.hip"), [], os.path.join(obj, "decode_model.o"))]
     for part in KERNEL_PARTS:
         jobs.append((os.path.join(CSRC, "moe_kernels.hip"), [f"-DMOE_PART={part}"],
                      os.path.join(obj, f"moe_kernels_part{part}.o")))
@@ -75,7 +77,23 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError(f"hipcc link failed ({r.returncode})")
     os.replace(tmp, LIB)
+    build_ck_shim(verbose)
     return LIB
+
+
+def build_ck_shim(verbose: bool = False) -> str:
+    """libck_gpu.so: host code only, linked against libmoe_gpu.so next to it (rpath $ORIGIN)."""
+    tmp = CK_LIB + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared", "-I", os.path.join(ROOT, "include"),
+           os.path.join(CSRC, "ck_shim.cpp"), "-L", LIBDIR, "-lmoe_gpu", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"hipcc failed on ck_shim.cpp ({r.returncode})")
+    os.replace(tmp, CK_LIB)
+    return CK_LIB
 
 
 if __name__ == "__main__":

@@ -246,9 +246,15 @@ size_t moe_attn_workspace_bytes(int n_q_heads, int head_dim, int S) {
 
 const char* moe_attn_last_error(void) { return t_err; }
 
-int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
-                        const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks the arguments and enqueues the three kernels with `workspace` (>= moe_attn_workspace_bytes bytes, device
+// memory) as the scores / partials buffer.
+int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace, size_t workspace_bytes,
+                void* stream) {
     if (head_dim != kD) return afail(MOE_GPU_EINVAL, "head_dim must be 128");
     const int G = n_kv_heads >= 1 && n_q_heads % n_kv_heads == 0 ? n_q_heads / n_kv_heads : 0;
     if (G != 1 && G != 2 && G != 4 && G != 8)
@@ -275,6 +281,17 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return afail(e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP, hipGetErrorString(e));
     return MOE_GPU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                        const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+    return attn_launch(n_q_heads, n_kv_heads, head_dim, S, scale, q, k_cache, v_cache, out, workspace, workspace_bytes,
+                       stream);
 }
 
 }  // extern "C"

@@ -3,6 +3,8 @@
 // main.rs:109-113 and :119: gemv(q/k/v/o_proj) followed by round_bf; main.rs:65-77: rope).
 #include <hip/hip_runtime.h>
 
+#include "ck_dot.h"
+#include "launch_util.h"
 #include "moe_gpu.h"
 
 namespace {
@@ -24,13 +26,33 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // y[m] = bf16(sum_k W[m, k] x[k]) for one token: x staged in LDS; waves take steps of RB whole rows, CG 16-byte
 // chunks per lane per load group, the next group's loads issued before the step's butterfly (the LM head's scheme).
+// norm_w != null: x is the residual stream and the GEMV reads rmsnorm(x, norm_w) (host.rs:71-76: ms = sum(x^2) / K in
+// fp32, r = 1 / sqrt(ms + eps), h = bf16(bf16(x * r) * w)), which every workgroup computes into LDS (the squares summed
+// per thread over its strided elements, then a 64-lane butterfly, then the 4 wavefronts in order): the layer's input
+// norm folded into its q|k|v projection.
 template <int RB, int CG>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
-                                                   uint16_t* __restrict__ y, int M, int K) {
+                                                   uint16_t* __restrict__ y, int M, int K,
+                                                   const uint16_t* __restrict__ norm_w, float eps) {
     extern __shared__ __align__(16) uint16_t xs[];
+    __shared__ float red[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int i = tid * 8; i < K; i += 256 * 8)
-        *reinterpret_cast<u32x4*>(&xs[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+    if (norm_w) {
+        float s = 0.f;
+        for (int i = tid; i < K; i += 256) {
+            const float v = bf2f(x[i]);
+            s = fmaf(v, v, s);
+        }
+        s = wave_sum(s);
+        if (lane == 0) red[wv] = s;
+        __syncthreads();
+        const float ms = (red[0] + red[1] + red[2] + red[3]) / (float)K;
+        const float r = 1.0f / sqrtf(ms + eps);
+        for (int i = tid; i < K; i += 256) xs[i] = (uint16_t)f2bf(bf2f(f2bf(bf2f(x[i]) * r)) * bf2f(norm_w[i]));
+    } else {
+        for (int i = tid * 8; i < K; i += 256 * 8)
+            *reinterpret_cast<u32x4*>(&xs[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+    }
     __syncthreads();
     const int nch = K / 512;
     const int gw = blockIdx.x * kWaves + wv, nw = gridDim.x * kWaves;
@@ -85,19 +107,71 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     }
 }
 
+// fp32 GEMV in the reference's ck_gemv order (ck_row_dot): y[m] = W[m] . x, bit-identical to ck_gemv (cpu_kern.c:31-35)
+// whenever no product or partial sum is a denormal.  Each wave takes one row per step, grid-strided; x is staged into
+// shared memory once per workgroup, after the first rows' loads are in flight.  LDS: K * 2 bytes of x, then the four
+// waves' 1 KiB segment buffers.
+__global__ __launch_bounds__(256) void gemv_ck_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+                                                      float* __restrict__ y, int M, int K) {
+    extern __shared__ __align__(16) uint16_t xs[];
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    moe::ckdot::lds_v4u* seg = (moe::ckdot::lds_v4u*)(xs + K) + wv * 64;
+    bool first = true;
+    for (int r0 = blockIdx.x * kWaves; r0 < M; r0 += gridDim.x * kWaves) {  // the same trip count in every wave
+        const int row = r0 + wv < M ? r0 + wv : M - 1;
+        float acc[1];
+        moe::ck_row_dot<1>(reinterpret_cast<const moe::ckdot::v4u*>(W + (size_t)row * K), K, 1, seg,
+                           (const moe::ckdot::lds_u32*)xs, acc, [&]() __attribute__((always_inline)) {
+                               if (first) {
+                                   for (int i = tid * 8; i < K; i += 256 * 8)
+                                       *reinterpret_cast<u32x4*>(&xs[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+                                   __syncthreads();
+                               }
+                           });
+        first = false;
+        if (lane == 0 && r0 + wv < M) y[r0 + wv] = acc[0];
+    }
+}
+
 // One workgroup per head, in place (main.rs:65-77): rot[i] = -x[i + D/2] for i < D/2, x[i - D/2] otherwise;
 // x[i] = bf16(bf16(x[i] * cos[i]) + bf16(rot[i] * sin[i])).  The head is staged in LDS first.
-__global__ __launch_bounds__(256) void rope_kernel(uint16_t* x, const uint16_t* cs, const uint16_t* sn, int D) {
-    __shared__ float old[1024];
-    uint16_t* xh = x + (size_t)blockIdx.x * D;
-    for (int i = threadIdx.x; i < D; i += blockDim.x) old[i] = bf2f(xh[i]);
+__device__ __forceinline__ void rope_head(const uint16_t* src, uint16_t* dst, const uint16_t* cs, const uint16_t* sn,
+                                          int D, float* old) {
+    for (int i = threadIdx.x; i < D; i += blockDim.x) old[i] = bf2f(src[i]);
     __syncthreads();
     const int half = D / 2;
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         const float rot = i < half ? -old[i + half] : old[i - half];
         const float a = bf2f(f2bf(old[i] * bf2f(cs[i])));
         const float b = bf2f(f2bf(rot * bf2f(sn[i])));
-        xh[i] = (uint16_t)f2bf(a + b);
+        dst[i] = (uint16_t)f2bf(a + b);
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(uint16_t* x, const uint16_t* cs, const uint16_t* sn, int D) {
+    __shared__ float old[1024];
+    uint16_t* xh = x + (size_t)blockIdx.x * D;
+    rope_head(xh, xh, cs, sn, D, old);
+}
+
+// The attention block's step between the q|k|v projection and attention (main.rs:112-118), one launch: workgroup h <
+// NQ ropes q head h in place; NQ <= h < NQ + NKV ropes k head h - NQ into the key cache row of position pos;
+// the last NKV workgroups copy the v heads into the value cache row.  qkv = [q (NQ*D) | k (NKV*D) | v (NKV*D)].
+__global__ __launch_bounds__(256) void rope_append_kernel(uint16_t* qkv, const uint16_t* cs, const uint16_t* sn,
+                                                          uint16_t* kc, uint16_t* vc, int NQ, int NKV, int D, int pos) {
+    __shared__ float old[1024];
+    const int h = blockIdx.x;
+    const size_t row = (size_t)pos * NKV * D;
+    if (h < NQ) {
+        uint16_t* xh = qkv + (size_t)h * D;
+        rope_head(xh, xh, cs, sn, D, old);
+    } else if (h < NQ + NKV) {
+        const int g = h - NQ;
+        rope_head(qkv + (size_t)(NQ + g) * D, kc + row + (size_t)g * D, cs, sn, D, old);
+    } else {
+        const int g = h - NQ - NKV;
+        const uint16_t* src = qkv + (size_t)(NQ + NKV + g) * D;
+        for (int i = threadIdx.x; i < D; i += blockDim.x) vc[row + (size_t)g * D + i] = src[i];
     }
 }
 
@@ -113,13 +187,13 @@ int gemv_grid(const void* fn, size_t lds, int M, int RB, int* grid) {
     static thread_local int n_cache = 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return MOE_GPU_EHIP;
+    // every launch checks the process-wide LDS limit (raised only, never lowered), independent of the occupancy cache
+    if (moe::raise_lds_limit(fn, lds) != hipSuccess) return MOE_GPU_EHIP;
     int wgs = 0;
     for (int i = 0; i < n_cache; ++i)
         if (cache[i].dev == dev && cache[i].fn == fn && cache[i].lds == lds) wgs = cache[i].wgs;
     if (wgs == 0) {
         int ncu = 0, per_cu = 0;
-        if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return MOE_GPU_EHIP;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MOE_GPU_EHIP;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) return MOE_GPU_EHIP;
         if (per_cu < 1) return MOE_GPU_EINVAL;
@@ -132,12 +206,13 @@ int gemv_grid(const void* fn, size_t lds, int M, int RB, int* grid) {
 }
 
 template <int RB, int CG>
-int gemv_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, int M, int K, hipStream_t st) {
+int gemv_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, int M, int K, const uint16_t* norm_w, float eps,
+                hipStream_t st) {
     const void* fn = reinterpret_cast<const void*>(&gemv_kernel<RB, CG>);
     const size_t lds = (size_t)K * sizeof(uint16_t);
     int grid = 0, rc = gemv_grid(fn, lds, M, RB, &grid);
     if (rc != MOE_GPU_OK) return rc;
-    hipLaunchKernelGGL((gemv_kernel<RB, CG>), dim3(grid), dim3(256), lds, st, W, x, y, M, K);
+    hipLaunchKernelGGL((gemv_kernel<RB, CG>), dim3(grid), dim3(256), lds, st, W, x, y, M, K, norm_w, eps);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_GPU_OK : e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
 }
@@ -146,14 +221,50 @@ int gemv_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, int M, int K,
 
 extern "C" {
 
-int moe_gemv_dev(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y, void* stream) {
+static int gemv_any(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y, const uint16_t* norm_w, float eps,
+                    void* stream) {
     if (M < 1 || K < 1024 || K % 1024 != 0 || K > 65536 || !W || !x || !y) return MOE_GPU_EINVAL;
     if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15) return MOE_GPU_EINVAL;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // whole 4096-column rows when K allows; 4 rows per wave step for tall W, 1 row for short W (1024 rows x 4 is a
     // quarter of the waves the chip holds)
-    if (K % 4096 == 0) return M >= 4096 ? gemv_launch<4, 8>(W, x, y, M, K, st) : gemv_launch<1, 8>(W, x, y, M, K, st);
-    return gemv_launch<8, 2>(W, x, y, M, K, st);
+    if (K % 4096 == 0)
+        return M >= 4096 ? gemv_launch<4, 8>(W, x, y, M, K, norm_w, eps, st) : gemv_launch<1, 8>(W, x, y, M, K, norm_w, eps, st);
+    return gemv_launch<8, 2>(W, x, y, M, K, norm_w, eps, st);
+}
+
+int moe_gemv_dev(int M, int K, const uint16_t* W, const uint16_t* x, uint16_t* y, void* stream) {
+    return gemv_any(M, K, W, x, y, nullptr, 0.f, stream);
+}
+
+int moe_gemv_f32_dev(int M, int K, const uint16_t* W, const uint16_t* x, float* y, void* stream) {
+    if (M < 1 || K < 512 || K % 512 != 0 || K > 65536 || !W || !x || !y) return MOE_GPU_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15) return MOE_GPU_EINVAL;
+    const void* fn = reinterpret_cast<const void*>(&gemv_ck_kernel);
+    const size_t lds = (size_t)K * 2 + (size_t)kWaves * 1024;
+    int grid = 0, rc = gemv_grid(fn, lds, M, 1, &grid);
+    if (rc != MOE_GPU_OK) return rc;
+    hipLaunchKernelGGL(gemv_ck_kernel, dim3(grid), dim3(256), lds, static_cast<hipStream_t>(stream), W, x, y, M, K);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? MOE_GPU_OK : e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
+}
+
+int moe_gemv_norm_dev(int M, int K, const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, float eps,
+                      uint16_t* y, void* stream) {
+    if (!norm_w || !(eps >= 0.f)) return MOE_GPU_EINVAL;
+    return gemv_any(M, K, W, x, y, norm_w, eps, stream);
+}
+
+int moe_rope_append_dev(int n_q_heads, int n_kv_heads, int head_dim, uint16_t* qkv, const uint16_t* cos_row,
+                        const uint16_t* sin_row, uint16_t* k_cache, uint16_t* v_cache, int pos, void* stream) {
+    if (n_q_heads < 1 || n_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024 || pos < 0 || !qkv ||
+        !cos_row || !sin_row || !k_cache || !v_cache)
+        return MOE_GPU_EINVAL;
+    hipLaunchKernelGGL(rope_append_kernel, dim3(n_q_heads + 2 * n_kv_heads), dim3(head_dim < 256 ? head_dim : 256), 0,
+                       static_cast<hipStream_t>(stream), qkv, cos_row, sin_row, k_cache, v_cache, n_q_heads,
+                       n_kv_heads, head_dim, pos);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? MOE_GPU_OK : e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
 }
 
 int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row, const uint16_t* sin_row,

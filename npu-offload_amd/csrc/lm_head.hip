@@ -12,6 +12,7 @@
 
 #include <string>
 
+#include "launch_util.h"
 #include "moe_gpu.h"
 
 namespace {
@@ -39,8 +40,14 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
     return u >> 16;
 }
 // 64-bit key whose unsigned order is (value, then lower row): the float's bits made order-preserving in the high
-// word, the complemented row in the low word.
-__device__ __forceinline__ unsigned long long key_of(float v, int row) {
+// word, the complemented row in the low word.  The reference's first-maximum loop (main.rs:384-385, `lg[i] > lg[best]`
+// from best = 0) treats -0 and +0 as equal, so -0 is keyed as +0; it never moves to a NaN and never leaves a NaN at row
+// 0, so a NaN ranks with -inf except at row 0, where it ranks above all (the pick is then row 0).  The chip's rule
+// (chip.rs:183-194, `val > best || (val == best && row < best_row)`) never picks a NaN: row0_nan_wins = false.
+__device__ __forceinline__ unsigned long long key_of(float v, int row, bool row0_nan_wins) {
+    if (v != v)
+        return row == 0 && row0_nan_wins ? ~0ull : ((unsigned long long)0x007FFFFFu << 32) | (uint32_t)(~(uint32_t)row);
+    if (v == 0.f) v = 0.f;
     const uint32_t b = __float_as_uint(v);
     const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)o << 32) | (uint32_t)(~(uint32_t)row);
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
                     if (row < V && t < T) {
                         if (a.logits && lane == r) a.logits[(size_t)t * V + row] = tot;
                         const float v = a.rule ? bf2f(f2bf(tot)) : tot;
-                        const unsigned long long k = key_of(v, row);
+                        const unsigned long long k = key_of(v, row, a.rule == 0);
                         best[t] = k > best[t] ? k : best[t];
                     }
                 }
@@ -255,10 +262,11 @@ int hfail(moe_head* h, int code, const char* fmt, ...) {
 
 template <int NT, int RB, int CG>
 int head_grid(moe_head* h, size_t lds, int* grid) {
+    const void* fn = reinterpret_cast<const void*>(&head_kernel<NT, RB, CG>);
+    // the limit is process-wide (another context's smaller table must not lower it): raised only, every launch
+    HCHK(h, moe::raise_lds_limit(fn, lds));
     if (h->grid[NT] == 0) {
-        const void* fn = reinterpret_cast<const void*>(&head_kernel<NT, RB, CG>);
         int ncu = 0, per_cu = 0;
-        HCHK(h, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         HCHK(h, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, h->device));
         HCHK(h, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds));
         if (per_cu < 1) return hfail(h, MOE_GPU_EINVAL, "head kernel does not fit a CU with %zu bytes of LDS", lds);

@@ -74,6 +74,9 @@ struct moe_gpu {
     int ksplit_shared = 0; // K parts per shared gate|up tile, 0 = automatic (MOE_GPU_OPT_KSPLIT_SHARED)
     int lag = 0;           // fused queue lag of down blocks, 0 = automatic (MOE_GPU_OPT_LAG)
     int shared_waits = 0;  // MOE_GPU_OPT_SHARED_WAITS
+    int grid_req = 0;      // fused grid override, 0 = automatic (MOE_GPU_OPT_GRID)
+    int router_poll = 1024;  // MOE_GPU_OPT_ROUTER_POLL
+    int route_rule = moe::kRouteSoftmax;  // MOE_GPU_OPT_ROUTE_RULE
     uint64_t* d_gpart = nullptr;    // tagged split gate|up partial sums
     unsigned epoch = 0;             // tag of the last call (tags are never 0)
     unsigned fused_launches = 0;    // selects the fused kernel's work-queue head
@@ -127,35 +130,60 @@ int check_layer(moe_gpu* c, int layer) {
     return MOE_GPU_OK;
 }
 
-// allocate (and zero) the bf16 tables of a layer on first use
-int ensure_layer(moe_gpu* c, int layer) {
+// Per-layer tables are allocated (and zeroed) on first use, each kind on its own: a layer whose routed experts are
+// only ever loaded as int8 holds no bf16 routed tables.
+void ensure_meta(moe_gpu* c, Layer& L) {
+    if (L.loaded.empty()) {
+        L.loaded.assign(c->d.E, 0);
+        L.loaded_q8.assign(c->d.E, 0);
+        L.shared_loaded.assign(c->d.n_shared, 0);
+    }
+}
+
+int ensure_router(moe_gpu* c, int layer) {
     Layer& L = c->layers[layer];
+    ensure_meta(c, L);
+    if (L.wr) return MOE_GPU_OK;
+    const Dims& d = c->d;
+    int rc;
+    if ((rc = dev_alloc(c, (void**)&L.wr, (size_t)d.E * d.H * 2, "router weight"))) return rc;
+    if ((rc = dev_alloc(c, (void**)&L.bias, (size_t)d.E * 4, "router bias"))) return rc;
+    HIPCHK(c, hipMemsetAsync(L.wr, 0, (size_t)d.E * d.H * 2, c->stream));
+    HIPCHK(c, hipMemsetAsync(L.bias, 0, (size_t)d.E * 4, c->stream));
+    return MOE_GPU_OK;
+}
+
+int ensure_bf16(moe_gpu* c, int layer) {
+    Layer& L = c->layers[layer];
+    ensure_meta(c, L);
     if (L.gu) return MOE_GPU_OK;
     const Dims& d = c->d;
     const size_t gub = d.gu_stride() * 2, dnb = d.dn_stride() * 2;
     int rc;
-    if ((rc = dev_alloc(c, (void**)&L.wr, (size_t)d.E * d.H * 2, "router weight"))) return rc;
-    if ((rc = dev_alloc(c, (void**)&L.bias, (size_t)d.E * 4, "router bias"))) return rc;
     if ((rc = dev_alloc(c, (void**)&L.gu, (size_t)d.E * gub, "gate|up tables"))) return rc;
     if ((rc = dev_alloc(c, (void**)&L.dn, (size_t)d.E * dnb, "down tables"))) return rc;
-    if (d.n_shared > 0) {
-        if ((rc = dev_alloc(c, (void**)&L.sgu, (size_t)d.n_shared * gub, "shared gate|up"))) return rc;
-        if ((rc = dev_alloc(c, (void**)&L.sdn, (size_t)d.n_shared * dnb, "shared down"))) return rc;
-        HIPCHK(c, hipMemsetAsync(L.sgu, 0, (size_t)d.n_shared * gub, c->stream));
-        HIPCHK(c, hipMemsetAsync(L.sdn, 0, (size_t)d.n_shared * dnb, c->stream));
-    }
-    HIPCHK(c, hipMemsetAsync(L.wr, 0, (size_t)d.E * d.H * 2, c->stream));
-    HIPCHK(c, hipMemsetAsync(L.bias, 0, (size_t)d.E * 4, c->stream));
     HIPCHK(c, hipMemsetAsync(L.gu, 0, (size_t)d.E * gub, c->stream));
     HIPCHK(c, hipMemsetAsync(L.dn, 0, (size_t)d.E * dnb, c->stream));
-    L.loaded.assign(d.E, 0);
-    L.loaded_q8.assign(d.E, 0);
-    L.shared_loaded.assign(d.n_shared, 0);
+    return MOE_GPU_OK;
+}
+
+int ensure_shared(moe_gpu* c, int layer) {
+    Layer& L = c->layers[layer];
+    ensure_meta(c, L);
+    if (L.sgu || c->d.n_shared == 0) return MOE_GPU_OK;
+    const Dims& d = c->d;
+    const size_t gub = d.gu_stride() * 2, dnb = d.dn_stride() * 2;
+    int rc;
+    if ((rc = dev_alloc(c, (void**)&L.sgu, (size_t)d.n_shared * gub, "shared gate|up"))) return rc;
+    if ((rc = dev_alloc(c, (void**)&L.sdn, (size_t)d.n_shared * dnb, "shared down"))) return rc;
+    HIPCHK(c, hipMemsetAsync(L.sgu, 0, (size_t)d.n_shared * gub, c->stream));
+    HIPCHK(c, hipMemsetAsync(L.sdn, 0, (size_t)d.n_shared * dnb, c->stream));
     return MOE_GPU_OK;
 }
 
 int ensure_q8(moe_gpu* c, int layer) {
     Layer& L = c->layers[layer];
+    ensure_meta(c, L);
     if (L.gu_q8) return MOE_GPU_OK;
     const Dims& d = c->d;
     int rc;
@@ -303,16 +331,22 @@ static int kparts_shared(const moe_gpu* c) {
 
 // The expert pipeline of one call.  do_topk: route on the device from the layer's router (ids/gates are outputs);
 // otherwise ids/gates are the caller's routing.  Fused: one persistent kernel; unfused: one kernel per phase.
-int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, float* gates, bool do_topk, int keep,
-              int n_shared, unsigned flags, float* out) {
+int run_layer(moe_gpu* c, int layer, int T, const moe::StageSrc& in, int32_t* ids, float* gates, bool do_topk,
+              int keep, int n_shared, unsigned flags, float* out, uint16_t* x_next = nullptr) {
     int rc;
+    // A call's epoch, queue head and cross-workgroup words are per launch: a captured launch replayed would read the
+    // previous replay's words as its own, so these calls refuse capture.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIPCHK(c, hipStreamIsCapturing(c->stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(c, MOE_GPU_ESTATE, "layer / moe calls cannot be captured into a graph (per-launch epochs and queue)");
     ExpertArgs a;
     a.L = ptrs(c, layer);
     a.d = c->d;
     a.T = T; a.keep = keep; a.n_shared = n_shared;
     a.int8 = (flags & MOE_GPU_INT8) ? 1 : 0;
     a.accumulate = (flags & MOE_GPU_ACCUMULATE) ? 1 : 0;
-    a.x = x; a.out = out; a.ids = ids; a.gates = gates;
+    a.in = in; a.out = out; a.x_next = x_next; a.ids = ids; a.gates = gates;
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
     a.kp = kparts(c);
@@ -325,42 +359,47 @@ int run_layer(moe_gpu* c, int layer, int T, const uint16_t* x, int32_t* ids, flo
         f.e = a;
         f.logits = c->d_logits_tag;
         f.sync = c->d_sync;
-        f.nR = do_topk ? (c->d.E + moe::kWaves - 1) / moe::kWaves : 0;
+        f.nR = do_topk ? (c->d.E + moe::kRouterRows - 1) / moe::kRouterRows : 0;
         f.do_topk = do_topk ? 1 : 0;
+        f.rule = c->route_rule;
+        f.router_poll = c->router_poll;
         f.trace = c->d_trace;
         f.lag = c->lag > 0 ? c->lag : 8;
         f.phase = (int)(c->fused_launches++ & 1u);
         f.shared_waits = c->shared_waits;
         c->trace_units = moe::fused_units(f.nR, a.maxs, c->d.n_shared, c->d.F, c->d.H, a.kp, a.kps);
-        LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->stream, &c->last_grid));
+        LAUNCH(c, K_FUSED, moe::launch_fused(f, c->wg_per_cu, c->grid_req, c->stream, &c->last_grid));
         return MOE_GPU_OK;
     }
     if (do_topk)
-        LAUNCH(c, K_ROUTER, moe::launch_router(a.L, c->d, T, x, c->d_logits_tag, nullptr, a.epoch, c->stream));
+        LAUNCH(c, K_ROUTER, moe::launch_router(a.L, c->d, T, a.in, c->d_logits_tag, nullptr, a.epoch, c->stream));
     // slots 0 .. d.n_shared-1 are always the shared experts' (summed only when this call includes them)
-    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, c->d.n_shared, do_topk, c->d_logits_tag, a.epoch,
-                                             a.err, ids, gates,
-                                             c->d_slots, c->stream));
+    LAUNCH(c, K_TOPK, moe::launch_topk_group(a.L, c->d, T, keep, c->d.n_shared, do_topk, c->route_rule,
+                                             c->d_logits_tag, a.epoch, a.err, ids, gates, c->d_slots, c->stream));
     LAUNCH(c, K_GATEUP, moe::launch_gateup(a, c->d_sync, c->stream));
     LAUNCH(c, K_DOWN, moe::launch_down(a, c->stream));
     return MOE_GPU_OK;
 }
 
+moe::StageSrc plain_src(const uint16_t* x) { return moe::StageSrc{x, nullptr, nullptr, nullptr, 0.f}; }
+
 int need_router(moe_gpu* c, int layer) {
     const Layer& L = c->layers[layer];
-    if (!L.gu || !L.router) return fail(c, MOE_GPU_ESTATE, "layer %d: router weights not loaded", layer);
-    if (L.n_loaded < c->d.E)
-        return fail(c, MOE_GPU_ESTATE, "layer %d: %d of %d routed experts loaded", layer, L.n_loaded, c->d.E);
+    if (!L.router) return fail(c, MOE_GPU_ESTATE, "layer %d: router weights not loaded", layer);
     return MOE_GPU_OK;
 }
 
+// all_routed: the call may reach any routed expert (device-side ids), so every one must be loaded in the precision
+// the call uses (a bf16 reload leaves an expert's int8 copy stale, and it then counts as not loaded)
 int need_experts(moe_gpu* c, int layer, unsigned flags, int with_shared, bool all_routed) {
     const Layer& L = c->layers[layer];
-    if (!L.gu) return fail(c, MOE_GPU_ESTATE, "layer %d: no experts loaded", layer);
-    if ((flags & MOE_GPU_INT8) && !L.gu_q8) return fail(c, MOE_GPU_ESTATE, "layer %d: no int8 experts loaded", layer);
-    if (all_routed && (flags & MOE_GPU_INT8) && L.n_loaded_q8 < c->d.E)
-        return fail(c, MOE_GPU_ESTATE, "layer %d: %d of %d routed experts have an int8 copy", layer, L.n_loaded_q8,
-                    c->d.E);
+    const bool q8 = (flags & MOE_GPU_INT8) != 0;
+    if (q8 ? !L.gu_q8 : !L.gu)
+        return fail(c, MOE_GPU_ESTATE, "layer %d: no %s routed experts loaded", layer, q8 ? "int8" : "bf16");
+    const int n = q8 ? L.n_loaded_q8 : L.n_loaded;
+    if (all_routed && n < c->d.E)
+        return fail(c, MOE_GPU_ESTATE, "layer %d: %d of %d routed experts loaded%s", layer, n, c->d.E,
+                    q8 ? " with a current int8 copy" : " in bf16");
     if (with_shared && L.n_shared_loaded < c->d.n_shared)
         return fail(c, MOE_GPU_ESTATE, "layer %d: %d of %d shared experts loaded", layer, L.n_shared_loaded,
                     c->d.n_shared);
@@ -494,7 +533,7 @@ static int load_expert_common(moe_gpu* c, int layer, int e, const uint16_t* g, c
     const int lim = shared ? c->d.n_shared : c->d.E;
     if (e < 0 || e >= lim) return fail(c, MOE_GPU_EINVAL, "%s expert %d outside [0, %d)", shared ? "shared" : "routed", e, lim);
     if (!g || !u || !d) return fail(c, MOE_GPU_EINVAL, "NULL weight pointer");
-    if ((rc = ensure_layer(c, layer))) return rc;
+    if ((rc = shared ? ensure_shared(c, layer) : ensure_bf16(c, layer))) return rc;
     Layer& L = c->layers[layer];
     const size_t n = (size_t)c->d.F * c->d.H;
     if (host) {
@@ -532,7 +571,7 @@ int moe_gpu_load_router(moe_gpu* c, int layer, const uint16_t* wr, const float* 
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
     if (!wr) return fail(c, MOE_GPU_EINVAL, "NULL router weight");
-    if ((rc = ensure_layer(c, layer))) return rc;
+    if ((rc = ensure_router(c, layer))) return rc;
     Layer& L = c->layers[layer];
     HIPCHK(c, hipMemcpyAsync(L.wr, wr, (size_t)c->d.E * c->d.H * 2, hipMemcpyHostToDevice, c->stream));
     if (bias) HIPCHK(c, hipMemcpyAsync(L.bias, bias, (size_t)c->d.E * 4, hipMemcpyHostToDevice, c->stream));
@@ -548,7 +587,7 @@ int moe_gpu_load_expert_q8(moe_gpu* c, int layer, int e, const int8_t* q, const 
     if ((rc = check_layer(c, layer))) return rc;
     if (e < 0 || e >= c->d.E) return fail(c, MOE_GPU_EINVAL, "routed expert %d outside [0, %d)", e, c->d.E);
     if (!q || !sc) return fail(c, MOE_GPU_EINVAL, "NULL int8 pointer");
-    if ((rc = ensure_layer(c, layer)) || (rc = ensure_q8(c, layer))) return rc;
+    if ((rc = ensure_q8(c, layer))) return rc;
     Layer& L = c->layers[layer];
     const Dims& d = c->d;
     HIPCHK(c, hipMemcpyAsync(c->d_stage_q8, q, (size_t)3 * d.F * d.H, hipMemcpyHostToDevice, c->stream));
@@ -568,6 +607,7 @@ int moe_gpu_quantize_experts(moe_gpu* c, int layer, int e0, int e1) {
     if (e0 < 0 || e1 > c->d.E || e0 >= e1) return fail(c, MOE_GPU_EINVAL, "expert range [%d, %d) invalid", e0, e1);
     Layer& L = c->layers[layer];
     if (!L.gu) return fail(c, MOE_GPU_ESTATE, "layer %d: no bf16 experts to quantise", layer);
+    ensure_meta(c, L);
     for (int e = e0; e < e1; e++)
         if (!L.loaded[e]) return fail(c, MOE_GPU_ESTATE, "layer %d: expert %d has no bf16 weights", layer, e);
     if ((rc = ensure_q8(c, layer))) return rc;
@@ -588,7 +628,8 @@ int moe_gpu_get_expert_q8(moe_gpu* c, int layer, int e, int8_t* q, float* sc) {
     if ((rc = check_layer(c, layer))) return rc;
     if (e < 0 || e >= c->d.E) return fail(c, MOE_GPU_EINVAL, "routed expert %d outside [0, %d)", e, c->d.E);
     Layer& L = c->layers[layer];
-    if (!L.gu_q8 || !L.loaded_q8[e]) return fail(c, MOE_GPU_ESTATE, "layer %d expert %d: no int8 copy", layer, e);
+    if (!L.gu_q8 || L.loaded_q8.empty() || !L.loaded_q8[e])
+        return fail(c, MOE_GPU_ESTATE, "layer %d expert %d: no int8 copy", layer, e);
     const Dims& d = c->d;
     HIPCHK(c, moe::launch_unlayout_q8(L.gu_q8 + (size_t)e * d.gu_stride(), L.dn_q8 + (size_t)e * d.dn_stride(),
                                       L.sc_q8 + (size_t)e * (2 * d.F + d.H), d.H, d.F, c->d_stage_q8, c->d_stage_sc,
@@ -611,26 +652,37 @@ int moe_gpu_route_dev(moe_gpu* c, int layer, int T, const uint16_t* x, int keep,
     unsigned ep = 0;
     if ((rc = next_epoch(c, &ep))) return rc;
     if ((rc = begin_timing(c))) return rc;
-    LAUNCH(c, K_ROUTER, moe::launch_router(L, c->d, T, x, c->d_logits_tag, logits, ep, c->stream));
-    LAUNCH(c, K_TOPK, moe::launch_topk_group(L, c->d, T, keep, c->d.n_shared, true, c->d_logits_tag, ep,
-                                             &c->d_sync->err, ids, gates, c->d_slots,
-                                             c->stream));
+    LAUNCH(c, K_ROUTER, moe::launch_router(L, c->d, T, plain_src(x), c->d_logits_tag, logits, ep, c->stream));
+    LAUNCH(c, K_TOPK, moe::launch_topk_group(L, c->d, T, keep, c->d.n_shared, true, c->route_rule, c->d_logits_tag,
+                                             ep, &c->d_sync->err, ids, gates, c->d_slots, c->stream));
     return end_timing(c);
 }
 
-int moe_gpu_moe_dev(moe_gpu* c, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates, int keep,
-                    int with_shared, unsigned flags, float* out) {
+}  // extern "C"
+
+// all_routed: the ids are on the device and unchecked, so every routed expert must be loaded in the call's precision;
+// the host entry point checks each id instead
+static int moe_dev_impl(moe_gpu* c, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates,
+                        int keep, int with_shared, unsigned flags, float* out, bool all_routed) {
     int rc = enter(c);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer)) || (rc = check_T(c, T)) || (rc = need_experts(c, layer, flags, with_shared, false)))
+    if ((rc = check_layer(c, layer)) || (rc = check_T(c, T)) ||
+        (rc = need_experts(c, layer, flags, with_shared, all_routed)))
         return rc;
     if (!x || !ids || !gates || !out) return fail(c, MOE_GPU_EINVAL, "NULL x/ids/gates/out");
     keep = norm_keep(c, keep);
     if ((rc = begin_timing(c))) return rc;
-    if ((rc = run_layer(c, layer, T, x, const_cast<int32_t*>(ids), const_cast<float*>(gates), false, keep,
+    if ((rc = run_layer(c, layer, T, plain_src(x), const_cast<int32_t*>(ids), const_cast<float*>(gates), false, keep,
                         with_shared ? c->d.n_shared : 0, flags, out)))
         return rc;
     return end_timing(c);
+}
+
+extern "C" {
+
+int moe_gpu_moe_dev(moe_gpu* c, int layer, int T, const uint16_t* x, const int32_t* ids, const float* gates, int keep,
+                    int with_shared, unsigned flags, float* out) {
+    return moe_dev_impl(c, layer, T, x, ids, gates, keep, with_shared, flags, out, true);
 }
 
 int moe_gpu_layer_dev(moe_gpu* c, int layer, int T, const uint16_t* x, int keep, unsigned flags, float* out,
@@ -645,7 +697,27 @@ int moe_gpu_layer_dev(moe_gpu* c, int layer, int T, const uint16_t* x, int keep,
     int32_t* di = ids ? ids : c->d_ids;
     float* dg = gates ? gates : c->d_gates;
     if ((rc = begin_timing(c))) return rc;
-    if ((rc = run_layer(c, layer, T, x, di, dg, true, keep, c->d.n_shared, flags, out))) return rc;
+    if ((rc = run_layer(c, layer, T, plain_src(x), di, dg, true, keep, c->d.n_shared, flags, out))) return rc;
+    return end_timing(c);
+}
+
+int moe_gpu_block_dev(moe_gpu* c, int layer, int T, const uint16_t* resid, const uint16_t* attn_o,
+                      const uint16_t* norm_w, float eps, int keep, unsigned flags, uint16_t* x_next, float* out,
+                      int32_t* ids, float* gates) {
+    int rc = enter(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_T(c, T)) || (rc = need_router(c, layer)) ||
+        (rc = need_experts(c, layer, flags, 1, true)))
+        return rc;
+    if (!resid || !attn_o || !norm_w || !x_next) return fail(c, MOE_GPU_EINVAL, "NULL resid/attn_o/norm_w/x_next");
+    if (flags & MOE_GPU_ACCUMULATE) return fail(c, MOE_GPU_EINVAL, "block calls write x_next; MOE_GPU_ACCUMULATE unsupported");
+    if (!(eps >= 0.f)) return fail(c, MOE_GPU_EINVAL, "eps must be >= 0");
+    keep = norm_keep(c, keep);
+    moe::StageSrc in{nullptr, resid, attn_o, norm_w, eps};
+    if ((rc = begin_timing(c))) return rc;
+    if ((rc = run_layer(c, layer, T, in, ids ? ids : c->d_ids, gates ? gates : c->d_gates, true, keep, c->d.n_shared,
+                        flags, out, x_next)))
+        return rc;
     return end_timing(c);
 }
 
@@ -681,7 +753,7 @@ int moe_gpu_moe(moe_gpu* c, int layer, int T, const uint16_t* x, const int32_t* 
                 return fail(c, MOE_GPU_EINVAL, "ids[%d][%d]=%d outside [-1, %d)", t, r, e, c->d.E);
             for (int r2 = 0; r2 < r; r2++)
                 if (ids[t * k + r2] == e) return fail(c, MOE_GPU_EINVAL, "token %d selects expert %d twice", t, e);
-            if (!L.gu || !((flags & MOE_GPU_INT8) ? L.loaded_q8[e] : L.loaded[e]))
+            if (L.loaded.empty() || !((flags & MOE_GPU_INT8) ? L.loaded_q8[e] : L.loaded[e]))
                 return fail(c, MOE_GPU_ESTATE, "layer %d: expert %d not loaded%s", layer, e,
                             (flags & MOE_GPU_INT8) ? " (int8)" : "");
         }
@@ -690,7 +762,8 @@ int moe_gpu_moe(moe_gpu* c, int layer, int T, const uint16_t* x, const int32_t* 
     HIPCHK(c, hipMemcpyAsync(c->d_gates, gates, (size_t)T * k * 4, hipMemcpyHostToDevice, c->stream));
     if (flags & MOE_GPU_ACCUMULATE)
         HIPCHK(c, hipMemcpyAsync(c->d_out, out, (size_t)T * c->d.H * 4, hipMemcpyHostToDevice, c->stream));
-    if ((rc = moe_gpu_moe_dev(c, layer, T, c->d_x, c->d_ids, c->d_gates, keep, with_shared, flags, c->d_out))) return rc;
+    if ((rc = moe_dev_impl(c, layer, T, c->d_x, c->d_ids, c->d_gates, keep, with_shared, flags, c->d_out, false)))
+        return rc;
     HIPCHK(c, hipMemcpyAsync(out, c->d_out, (size_t)T * c->d.H * 4, hipMemcpyDeviceToHost, c->stream));
     return sync_and_check(c);
 }
@@ -725,7 +798,9 @@ int moe_gpu_synth_fill(moe_gpu* c, uint16_t* dst, uint64_t n, uint64_t key, uint
 int moe_gpu_synth_layer(moe_gpu* c, int layer, uint64_t seed, float cw, const float* bias) {
     int rc = enter(c);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer)) || (rc = ensure_layer(c, layer))) return rc;
+    if ((rc = check_layer(c, layer)) || (rc = ensure_router(c, layer)) || (rc = ensure_bf16(c, layer)) ||
+        (rc = ensure_shared(c, layer)))
+        return rc;
     Layer& L = c->layers[layer];
     const Dims& d = c->d;
     auto tid = [&](int e, int m) { return ((uint64_t)layer * 4096 + (uint64_t)e) * 4 + (uint64_t)m; };
@@ -784,6 +859,19 @@ int moe_gpu_set_option(moe_gpu* c, int opt, int value) {
             c->lag = value;
             return MOE_GPU_OK;
         case MOE_GPU_OPT_SHARED_WAITS: c->shared_waits = value != 0; return MOE_GPU_OK;
+        case MOE_GPU_OPT_GRID:
+            if (value < 0) return fail(c, MOE_GPU_EINVAL, "grid %d < 0", value);
+            c->grid_req = value;
+            return MOE_GPU_OK;
+        case MOE_GPU_OPT_ROUTER_POLL:
+            if (value < 0) return fail(c, MOE_GPU_EINVAL, "router poll %d < 0", value);
+            c->router_poll = value;
+            return MOE_GPU_OK;
+        case MOE_GPU_OPT_ROUTE_RULE:
+            if (value != MOE_GPU_ROUTE_SOFTMAX && value != MOE_GPU_ROUTE_SIGMOID)
+                return fail(c, MOE_GPU_EINVAL, "route rule %d not MOE_GPU_ROUTE_SOFTMAX / _SIGMOID", value);
+            c->route_rule = value == MOE_GPU_ROUTE_SIGMOID ? moe::kRouteSigmoid : moe::kRouteSoftmax;
+            return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
 }
@@ -792,7 +880,7 @@ int moe_gpu_trace_units(moe_gpu* c, int on) {
     int rc = enter(c);
     if (rc) return rc;
     if (on && !c->d_trace) {
-        const size_t units = (size_t)moe::fused_units((c->d.E + moe::kWaves - 1) / moe::kWaves,
+        const size_t units = (size_t)moe::fused_units((c->d.E + moe::kRouterRows - 1) / moe::kRouterRows,
                                                       c->d.n_shared + c->d.max_t * c->d.k, c->d.n_shared, c->d.F,
                                                       c->d.H, moe::kMaxKp, moe::kMaxKp);
         const size_t bytes = units * moe::kTraceFields * sizeof(uint64_t);
@@ -830,6 +918,11 @@ int moe_gpu_get_option(moe_gpu* c, int opt, int* value) {
         case MOE_GPU_OPT_LAG: *value = c->lag; return MOE_GPU_OK;
         case MOE_GPU_OPT_SHARED_WAITS: *value = c->shared_waits; return MOE_GPU_OK;
         case MOE_GPU_OPT_KSPLIT_SHARED: *value = c->ksplit_shared; return MOE_GPU_OK;
+        case MOE_GPU_OPT_GRID: *value = c->grid_req; return MOE_GPU_OK;
+        case MOE_GPU_OPT_ROUTER_POLL: *value = c->router_poll; return MOE_GPU_OK;
+        case MOE_GPU_OPT_ROUTE_RULE:
+            *value = c->route_rule == moe::kRouteSigmoid ? MOE_GPU_ROUTE_SIGMOID : MOE_GPU_ROUTE_SOFTMAX;
+            return MOE_GPU_OK;
         default: return fail(c, MOE_GPU_EINVAL, "unknown option %d", opt);
     }
 }

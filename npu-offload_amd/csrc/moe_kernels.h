@@ -16,6 +16,10 @@ constexpr int kMaxTopk = 8;
 constexpr int kMaxShared = 4;
 constexpr int kMaxExperts = 512;
 constexpr int kMaxSlots = kMaxShared + kMaxTokens * kMaxTopk;
+constexpr int kRouterRows = 4;     // router rows per router unit: one per wavefront
+
+// Routing rules of the compute calls (the flag bits MOE_GPU_ROUTE_* of the C ABI select them).
+enum RouteRule { kRouteSoftmax = 0, kRouteSigmoid = 1 };
 
 // Per-call expert grouping, built on the device: slot s < n_shared is shared expert s (expert = -1 - s) over all
 // tokens; routed slots follow in first-seen order scanning tokens then ranks (solar_hybrid/runtime.py:344-347).
@@ -63,14 +67,26 @@ __host__ __device__ inline int gu_row_up(int i) { return (i >> 3) & 1; }
 constexpr int kMaxHTiles = 256;  // H <= 16384 (64-row down tiles)
 constexpr int kMaxKp = 4;        // K parts of a gate|up tile
 
+// Where a call's token activations come from.  x: the MoE input [T][H] bf16 as given.  Block mode (resid != null,
+// a decode layer's second half, track2_opt/solar_engine/src/main.rs:120-124): the input is
+// rmsnorm(bf16(resid + attn_o), norm_w) (host.rs:71-76), computed by every workgroup that stages it.
+struct StageSrc {
+    const uint16_t* x;       // [T][H] bf16, or null in block mode
+    const uint16_t* resid;   // [T][H] bf16 residual stream before the attention output is added
+    const uint16_t* attn_o;  // [T][H] bf16 attention block output (o_proj, rounded)
+    const uint16_t* norm_w;  // [H] bf16 post-attention RMSNorm weight
+    float eps;
+};
+
 // Everything one expert pipeline call needs (device pointers).
 struct ExpertArgs {
     LayerPtrs L;
     Dims d;
     int T, keep, n_shared, int8, accumulate;  // n_shared: shared experts summed in this call (0 or d.n_shared)
     int maxs;                                 // slots this call can use: d.n_shared + T * keep
-    const uint16_t* x;                        // [T][H] bf16
-    float* out;                               // [T][H] fp32
+    StageSrc in;                              // the tokens' activations
+    float* out;                               // [T][H] fp32, or null in block mode
+    uint16_t* x_next;                         // block mode: the next residual [T][H] bf16, else null
     int32_t* ids;                             // [T][k]
     float* gates;                             // [T][k]
     Slots* slots;
@@ -86,7 +102,8 @@ struct ExpertArgs {
 
 // Work-queue heads of the fused kernel.  Fused launch n (the host counts them) hands out units from
 // next_unit[n & 1] and clears next_unit[(n + 1) & 1] for the next launch; the unfused path clears both.  Each head
-// sits in its own 128-byte line.
+// sits in its own 128-byte line.  Workgroup b < min(grid, router units) runs router unit b first; every other unit
+// is handed out by the queue, in ascending order, to a running workgroup.
 constexpr int kSyncPad = 32;  // unsigneds per line
 struct Sync {
     unsigned err;  // set when a bounded wait gave up (sticky until the host clears it)
@@ -107,9 +124,14 @@ struct FusedArgs {
     uint64_t* trace;  // optional: per unit {start, dependencies met, end, workgroup} in 100 MHz realtime ticks
     int nR;         // router units (0 when the caller gives ids)
     int do_topk;
+    int rule;       // RouteRule
     int phase;      // work-queue head of this launch (fused launch count & 1)
     int lag;        // queue order: routed slot s's down block follows routed slot (s + lag)'s gate|up block (lag >= 1)
     int shared_waits;  // 1: shared gate|up parts start only once the routing is known
+    // passes of the bounded wait for the router logits before a workgroup computes the missing router rows itself
+    // (a router unit whose workgroup is not resident never blocks the routing); 0: compute them as soon as one is
+    // missing at the first look
+    int router_poll;
 };
 
 // Fused-kernel unit count: router units, the route publisher, then every slot's gate|up and down units (S shared
@@ -126,9 +148,9 @@ size_t lds_bytes(int T, int NT, int H, int F, int E);
 
 // ---- launch helpers (moe_kernels.hip) ---------------------------------------------------------------------------
 // logits: tagged [T][E] (always written); logits_out: optional plain fp32 copy
-hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, uint64_t* logits,
+hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const StageSrc& in, uint64_t* logits,
                          float* logits_out, unsigned epoch, hipStream_t st);
-hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
+hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk, int rule,
                              const uint64_t* logits, unsigned epoch, unsigned* err, int32_t* ids, float* gates,
                              Slots* slots, hipStream_t st);
 // gate|up parts; also clears the fused work-queue heads (the unfused path does not use them)
@@ -136,8 +158,8 @@ hipError_t launch_gateup(const ExpertArgs& a, Sync* sync, hipStream_t st);
 // down projection + the gated combine (the down unit of the last slot combines each 64-row tile)
 hipError_t launch_down(const ExpertArgs& a, hipStream_t st);
 // wg_per_cu <= 0: as many workgroups per CU as fit (a plain launch: the work queue needs no co-residency);
-// grid_out receives the grid size
-hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out);
+// grid > 0 overrides the grid size (it may exceed what fits at once); grid_out receives the grid size
+hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, int grid, hipStream_t st, int* grid_out);
 
 hipError_t launch_relayout_gu(const uint16_t* g, const uint16_t* u, int H, int F, uint16_t* dst, hipStream_t st);
 hipError_t launch_relayout_dn(const uint16_t* d, int H, int F, uint16_t* dst, hipStream_t st);

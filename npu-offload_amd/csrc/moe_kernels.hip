@@ -17,6 +17,9 @@
 
 #include <math.h>
 
+#include "ck_dot.h"
+#include "launch_util.h"
+
 namespace moe {
 
 // Build partitioning.  Compiled as one translation unit (MOE_PART undefined), or as parts compiled in parallel:
@@ -93,15 +96,16 @@ __device__ __forceinline__ bool tag_ok(uint64_t w, unsigned epoch) { return (uns
 // together, one round trip per pass, until all do.  Gives up after kSpinLimit passes, or early once another wait of
 // the launch gave up (err set), so no wait can hang the GPU; the host then reports the call as failed.
 template <int M, typename Ptr, typename Need>
-__device__ __forceinline__ void settle(uint64_t (&w)[M], Ptr ptr, Need need, unsigned epoch, unsigned* err) {
-    auto pending = [&]() {
-        bool p = false;
+__device__ __forceinline__ bool pending_words(const uint64_t (&w)[M], Need need, unsigned epoch) {
+    bool p = false;
 #pragma unroll
-        for (int m = 0; m < M; m++) p = p || (need(m) && !tag_ok(w[m], epoch));
-        return p;
-    };
+    for (int m = 0; m < M; m++) p = p || (need(m) && !tag_ok(w[m], epoch));
+    return p;
+}
+template <int M, typename Ptr, typename Need>
+__device__ __forceinline__ void settle(uint64_t (&w)[M], Ptr ptr, Need need, unsigned epoch, unsigned* err) {
     unsigned n = 0;
-    while (pending()) {
+    while (pending_words<M, Ptr>(w, need, epoch)) {
         ++n;
         if (n > kSpinLimit || ((n & 255) == 0 && ld_sync(err))) {
             st_sync(err, 1u);
@@ -112,6 +116,18 @@ __device__ __forceinline__ void settle(uint64_t (&w)[M], Ptr ptr, Need need, uns
         for (int m = 0; m < M; m++)
             if (need(m) && !tag_ok(w[m], epoch)) w[m] = ld_sync(ptr(m));
     }
+}
+// The same wait bounded by `limit` passes, without flagging an error: returns false when words are still missing.
+template <int M, typename Ptr, typename Need>
+__device__ __forceinline__ bool settle_for(uint64_t (&w)[M], Ptr ptr, Need need, unsigned epoch, int limit) {
+    for (int n = 0; pending_words<M, Ptr>(w, need, epoch); ++n) {
+        if (n >= limit) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            if (need(m) && !tag_ok(w[m], epoch)) w[m] = ld_sync(ptr(m));
+    }
+    return true;
 }
 
 // wavefront index within the workgroup as a wave-uniform (scalar) value, so loop bounds derived from it stay scalar
@@ -306,73 +322,123 @@ __device__ inline Lds lds_carve(unsigned char* base_generic, int T, int NT, int 
     return s;
 }
 
-__device__ inline void stage_x(const Lds& s, const uint16_t* __restrict__ x, int T, int H) {
+__device__ __forceinline__ float round_bf(float v) { return bf_lo(f2bf_dev(v)); }
+
+__device__ __forceinline__ u32x4 pack_bf16x8(const float* v) {
+    u32x4 r;
+    r.x = f2bf_dev(v[0]) | ((unsigned)f2bf_dev(v[1]) << 16);
+    r.y = f2bf_dev(v[2]) | ((unsigned)f2bf_dev(v[3]) << 16);
+    r.z = f2bf_dev(v[4]) | ((unsigned)f2bf_dev(v[5]) << 16);
+    r.w = f2bf_dev(v[6]) | ((unsigned)f2bf_dev(v[7]) << 16);
+    return r;
+}
+
+// Stage the T tokens' activations into s.xs (every thread returns after the closing barrier).
+//   plain: a copy of in.x;
+//   block mode: r = bf16(resid + attn_o) (main.rs:122), then RMSNorm (host.rs:71-76): ms = sum(r^2) / H,
+//   rs = 1 / sqrt(ms + eps), h = bf16(bf16(r * rs) * w).  The squares are summed in a fixed order (per thread over
+//   its chunks in order, then a 64-lane xor butterfly, then the 4 wavefronts in order), so every workgroup stages
+//   the same bits.  Each thread handles 16-byte chunks c = tid + j * kThreads, two per pass (H = 4096: one pass, one
+//   round trip for resid, attn_o and the norm weight together), with few registers: the router unit stages while
+//   its weight loads are held in registers.
+__device__ __forceinline__ void stage_in(const Lds& s, const StageSrc& in, int T, int H) {
     const int n = T * (H / 8);
-    const u32x4* src = reinterpret_cast<const u32x4*>(x);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) s.xs[i] = src[i];
+    if (!in.resid) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(in.x);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) s.xs[i] = src[i];
+        __syncthreads();
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), nc = H / 8;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(in.resid);
+    const u32x4* xo = reinterpret_cast<const u32x4*>(in.attn_o);
+    const u32x4* wn = reinterpret_cast<const u32x4*>(in.norm_w);
+    const bool w_held = nc <= 2 * kThreads;  // the norm weights of this thread's chunks stay in registers
+    u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = {0u, 0u, 0u, 0u};
+    if (w_held) {
+        if (tid < nc) w0 = wn[tid];
+        if (tid + kThreads < nc) w1 = wn[tid + kThreads];
+    }
+    for (int t = 0; t < T; t++) {
+        float sq = 0.f;
+        for (int c0 = tid; c0 < nc; c0 += 2 * kThreads) {
+            const int c1 = c0 + kThreads;
+            const u32x4 a0 = xr[(size_t)t * nc + c0], b0 = xo[(size_t)t * nc + c0];
+            u32x4 a1 = a0, b1 = b0;
+            if (c1 < nc) {
+                a1 = xr[(size_t)t * nc + c1];
+                b1 = xo[(size_t)t * nc + c1];
+            }
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                if (h == 1 && c1 >= nc) break;
+                float fa[8], fb[8], r[8];
+                unpack8(h ? a1 : a0, fa);
+                unpack8(h ? b1 : b0, fb);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    r[i] = round_bf(fa[i] + fb[i]);  // main.rs:122
+                    sq = fmaf(r[i], r[i], sq);
+                }
+                s.xs[t * nc + (h ? c1 : c0)] = pack_bf16x8(r);
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) sq = sq + __shfl_xor(sq, m, 64);
+        if (lane == 0) s.red[t * kWaves + wave] = sq;
+    }
+    __syncthreads();
+    for (int t = 0; t < T; t++) {
+        const float ms = (((s.red[t * kWaves] + s.red[t * kWaves + 1]) + s.red[t * kWaves + 2]) + s.red[t * kWaves + 3]) /
+                         (float)H;
+        const float rs = 1.0f / sqrtf(ms + in.eps);
+        for (int c = tid; c < nc; c += kThreads) {
+            const u32x4 wv = w_held ? (c == tid ? w0 : w1) : wn[c];
+            float fr[8], fw[8], h[8];
+            unpack8(s.xs[t * nc + c], fr);
+            unpack8(wv, fw);
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[i] = round_bf(round_bf(fr[i] * rs) * fw[i]);
+            s.xs[t * nc + c] = pack_bf16x8(h);
+        }
+    }
     __syncthreads();
 }
 
+// Outputs of one combined element o = t * H + h: out (fp32, when given) and, in block mode, the next residual
+// x = bf16(r + bf16(bf16(routed) + bf16(shared))) with r = bf16(resid + attn_o), as the host layer's moe_host
+// (main.rs:133-141: the shared and the routed sums each rounded to bf16, their sum rounded, added to the residual).
+__device__ __forceinline__ void combine_store(const ExpertArgs& a, size_t o, float acc, float acc_s, float acc_r) {
+    if (a.out) a.out[o] = acc;
+    if (a.x_next) {
+        const float r = round_bf(bf_lo(a.in.resid[o]) + bf_lo(a.in.attn_o[o]));
+        a.x_next[o] = f2bf_dev(r + round_bf(round_bf(acc_r) + round_bf(acc_s)));
+    }
+}
+
 // --------------------------------------------------------------------------------------------------------------------
-// Unit: router rows.  Wave w computes logits[t, e] for e = e0 + w and all T tokens.  Reduction order (mirrored bit
-// for bit by the host oracle): lane l owns chunks c = l + 64 j; per token a fused multiply-add chain over j
-// ascending and elements 0..7 ascending; then a 64-lane xor butterfly (32, 16, 8, 4, 2, 1).
-// x_stage: when not null the activations are staged here, after the first block of weight loads is in flight.
+// Unit: router rows, in the reference's own order (ck_row_dot, ck_dot.h): the logits are bit-identical to ck_gemv's
+// (track2_opt/solar_engine/csrc/cpu_kern.c:9-19, :31-35).  Wave w computes row e0 + w for all T tokens; its 1 KiB
+// segment buffer is carved from s.as, unused while a router unit runs.
+// stage: the activations (from src) are staged once the weight loads are in flight.  src travels by value: an
+// address of a kernel argument would make the compiler copy the arguments to scratch memory.
 template <int NT>
 __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
                                             uint64_t* __restrict__ logits, float* __restrict__ logits_out,
-                                            unsigned epoch, const uint16_t* __restrict__ x_stage) {
+                                            unsigned epoch, bool stage, const StageSrc src) {
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int e = e0 + wave;
-    const u32x4* row = reinterpret_cast<const u32x4*>(wr + (size_t)min(e, E - 1) * H);
-    const int nc = H / 8, nj = H / 512;
     float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = 0.f;
-    u32x4 w[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (j < nj) w[j] = row[lane + 64 * j];
-    if (x_stage) stage_x(s, x_stage, T, H);
-    for (int j0 = 0; j0 < nj; j0 += 8) {
-        if (j0 > 0) {
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (j0 + j < nj) w[j] = row[lane + 64 * (j0 + j)];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (j0 + j < nj) {
-                float wf[8];
-                unpack8(w[j], wf);
-                const int c = lane + 64 * (j0 + j);
-                // all NT columns, with no per-token branch (columns t >= T read token 0 and are discarded), so the
-                // shared-memory reads of a chunk are all in flight together
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    float xf[8];
-                    unpack8(s.xs[(t < T ? t : 0) * nc + c], xf);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) acc[t] = fmaf(wf[i], xf[i], acc[t]);
-                }
-            }
-        }
-    }
-    if (e >= E) return;
-    float v[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) v[t] = acc[t];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) v[t] = v[t] + __shfl_xor(v[t], m, 64);
-    }
-    if (lane == 0) {
+    ck_row_dot<NT>(reinterpret_cast<const u32x4*>(wr + (size_t)min(e, E - 1) * H), H, T, s.as + wave * 64,
+                   (const LDS_AS unsigned*)s.xs, acc, [&]() __attribute__((always_inline)) {
+                       if (stage) stage_in(s, src, T, H);
+                   });
+    if (lane == 0 && e < E) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (t < T) {
-                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(v[t]));
-                if (logits_out) logits_out[(size_t)t * E + e] = v[t];
+                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(acc[t]));
+                if (logits_out) logits_out[(size_t)t * E + e] = acc[t];
             }
         }
     }
@@ -408,17 +474,31 @@ __device__ __forceinline__ float route_key_score(uint64_t key) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-// Softmax top-k and expert grouping into rt.  Selection: the k largest keys (score descending, index ascending);
-// each thread counts, for one (token, expert) and a slice of the experts, how many keys beat it (its rank), reading
-// the keys as shared-memory broadcasts, so the whole workgroup works on it.  Gates = softmax restricted to the kept
-// ranks: exp(s_r - s_0) / sum_{q < keep} exp(s_q - s_0), summed in rank order.  Grouping: routed slots in first-seen
-// order scanning tokens then ranks (solar_hybrid/runtime.py:344-347), after the n_shared shared slots.  do_topk == 0:
-// the caller's ids / gates are taken as given (ids outside [-1, E) dropped).  scr: kRouteScratchBytes of LDS.
-__device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned char* scr,
-                                            const uint64_t* __restrict__ logits, unsigned epoch, unsigned* err,
-                                            const float* __restrict__ bias, const int32_t* ids_in,
-                                            const float* gates_in, int T, int E, int k, int keep, int n_shared,
-                                            int do_topk) {
+// sigmoid of a logit as the reference's route() computes it in fp32 (host.rs:119-121: 1 / (1 + exp(-v))).  exp is
+// evaluated in double and rounded once to fp32, which is the correctly rounded fp32 exp except when the value lies
+// within a double rounding error of an fp32 rounding boundary; the add and the divide are single IEEE operations.
+__device__ __forceinline__ float sigmoid_ref(float v) {
+    const float ex = (float)exp(-(double)v);
+    return 1.f / (1.f + ex);
+}
+
+// Top-k and expert grouping into rt.  Selection: the k largest keys (score descending, index ascending); each thread
+// counts, for one (token, expert) and a slice of the experts, how many keys beat it (its rank), reading the keys as
+// shared-memory broadcasts, so the whole workgroup works on it.  Scores and gates by rule:
+//   softmax (npu-kernels/npu_kernels/rngd/layer_template/src/host.rs.tpl:247-267): score = logit + bias; gates = the
+//     softmax restricted to the kept ranks, exp(s_r - s_0) / sum_{q < keep} exp(s_q - s_0), summed in rank order;
+//   sigmoid (track2_opt/solar_engine/src/host.rs:119-128): s = sigmoid(logit), score = s + bias (the bias only
+//     selects); gates = s_r / (sum_{q < keep} s_q + 1e-20), summed in rank order.
+// Grouping: routed slots in first-seen order scanning tokens then ranks (solar_hybrid/runtime.py:344-347), after the
+// n_shared shared slots.  do_topk == 0: the caller's ids / gates are taken as given (ids outside [-1, E) dropped).
+// scr: kRouteScratchBytes of LDS.  poll >= 0 bounds the wait for the tagged logits to that many passes: the call then
+// returns 1, uniformly, when logits are still missing (their router units have not run), and the caller computes
+// them itself and calls again; poll < 0 waits up to the launch-wide limit.  Returns 0 once rt is complete.
+__device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned char* scr,
+                                           const uint64_t* __restrict__ logits, unsigned epoch, unsigned* err,
+                                           const float* __restrict__ bias, const int32_t* ids_in,
+                                           const float* gates_in, int T, int E, int k, int keep, int n_shared,
+                                           int do_topk, int rule, int poll) {
     const int tid = threadIdx.x, nthr = blockDim.x;
     LDS_AS uint64_t* keys = (LDS_AS uint64_t*)scr;
     LDS_AS int* cnt = (LDS_AS int*)(scr + (size_t)kRouteKeys * 8);
@@ -443,12 +523,19 @@ __device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned ch
                     b[m] = bias ? bias[(tid + m * nthr) % E] : 0.f;
                 }
             }
-            settle(w, lptr, lneed, epoch, err);
+            if (poll < 0) {
+                settle(w, lptr, lneed, epoch, err);
+            } else if (__syncthreads_or(!settle_for(w, lptr, lneed, epoch, poll))) {
+                return 1;
+            }
+            float sg[M];  // sigmoid rule: the unbiased scores (the gates' numerators)
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 if (lneed(m)) {
                     const int i = tid + m * nthr;
-                    float v = __uint_as_float((unsigned)w[m]) + b[m];
+                    const float lg = __uint_as_float((unsigned)w[m]);
+                    sg[m] = rule == kRouteSigmoid ? sigmoid_ref(lg) : 0.f;
+                    float v = (rule == kRouteSigmoid ? sg[m] : lg) + b[m];
                     if (!(v == v)) v = -INFINITY;
                     if (v == 0.f) v = 0.f;  // -0 and +0 compare equal: one key
                     keys[i] = route_key(v, i % E);
@@ -477,14 +564,19 @@ __device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned ch
                 cnt[wi] = c;
             }
             __syncthreads();
-            // 3. the k best of each token, in rank order (gate slot holds the score until step 4)
-            for (int i = tid; i < items; i += nthr) {
-                int r = 0;
-                for (int p = 0; p < parts; p++) r += cnt[p * items + i];
-                if (r < k) {
-                    const int t = t0 + i / E;
-                    rt->id[t * k + r] = i % E;
-                    rt->gate[t * k + r] = route_key_score(keys[i]);
+            // 3. the k best of each token, in rank order (the gate slot holds the score until step 4: the biased
+            //    score for softmax, the unbiased sigmoid for sigmoid)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int i = tid + m * nthr;
+                if (i < items) {
+                    int r = 0;
+                    for (int p = 0; p < parts; p++) r += cnt[p * items + i];
+                    if (r < k) {
+                        const int t = t0 + i / E;
+                        rt->id[t * k + r] = i % E;
+                        rt->gate[t * k + r] = rule == kRouteSigmoid ? sg[m] : route_key_score(keys[i]);
+                    }
                 }
             }
             __syncthreads();
@@ -493,11 +585,18 @@ __device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned ch
             for (int tl = wave; tl < nt; tl += nthr / 64) {
                 const int t = t0 + tl;
                 const float sc = lane < k ? rt->gate[t * k + lane] : 0.f;
-                const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), 0));
-                const float ex = expf(sc - top);
-                float tot = 0.f;
-                for (int q = 0; q < keep; q++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), q));
-                if (lane < k) rt->gate[t * k + lane] = lane < keep ? ex / tot : 0.f;
+                if (rule == kRouteSigmoid) {
+                    float tot = 0.f;
+                    for (int q = 0; q < keep; q++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), q));
+                    tot = tot + 1e-20f;
+                    if (lane < k) rt->gate[t * k + lane] = lane < keep ? sc / tot : 0.f;
+                } else {
+                    const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), 0));
+                    const float ex = expf(sc - top);
+                    float tot = 0.f;
+                    for (int q = 0; q < keep; q++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), q));
+                    if (lane < k) rt->gate[t * k + lane] = lane < keep ? ex / tot : 0.f;
+                }
                 if (T == 1) {  // one token's k distinct experts: slot n_shared + r holds rank r (closed-form grouping)
                     if (lane < keep) {
                         const int sl = n_shared + lane;
@@ -533,7 +632,7 @@ __device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned ch
     }
     if (do_topk && T == 1) {  // grouped above
         __syncthreads();
-        return;
+        return 0;
     }
     bad = __syncthreads_or(bad);
     // Grouping: thread p owns entry p = t * keep + r (n = T * keep <= 128); entries are compared through shared-memory
@@ -616,6 +715,7 @@ __device__ __forceinline__ void route_local(lds_RouteTab* rt, LDS_AS unsigned ch
         if (64 + lane < nr) rt->slot_pair[n_shared + 64 + lane] = (short)(n_shared * T + tot0 + i1 - c1);
     }
     __syncthreads();
+    return 0;
 }
 
 // Write the routing outputs (ids / gates when computed here) and the global slot table used by the unfused kernels.
@@ -867,15 +967,19 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
         for (int i = threadIdx.x; i < ne; i += blockDim.x) {  // fixed order: shared terms, then ranks
             const int t = i / 64;
             const size_t o = (size_t)t * H + ht * 64 + i % 64;
-            float acc2 = a.accumulate ? a.out[o] : 0.f;
+            float acc2 = a.accumulate ? a.out[o] : 0.f, acc_s = 0.f, acc_r = 0.f;
             for (int q = 0; q < kq; q++) {
                 if (q < S) {
-                    if (q < a.n_shared) acc2 = acc2 + cv[q * ne + i];
+                    if (q < a.n_shared) {
+                        acc2 = acc2 + cv[q * ne + i];
+                        acc_s = acc_s + cv[q * ne + i];
+                    }
                 } else if (q - S < a.keep && crt->id[t * k + q - S] >= 0) {
                     acc2 = fmaf(crt->gate[t * k + q - S], cv[q * ne + i], acc2);
+                    acc_r = fmaf(crt->gate[t * k + q - S], cv[q * ne + i], acc_r);
                 }
             }
-            a.out[o] = acc2;
+            combine_store(a, o, acc2, acc_s, acc_r);
         }
     }
     __syncthreads();  // s.as / s.red are reused by the next unit
@@ -908,17 +1012,22 @@ __device__ __forceinline__ void combine_tile(const ExpertArgs& a, const lds_Rout
             if (ylive(q)) w[q] = ld_sync(yptr(q));
         settle(w, yptr, ylive, a.epoch, a.err);
         const size_t o = (size_t)t * H + h;
-        float acc = a.accumulate ? a.out[o] : 0.f;
+        float acc = a.accumulate ? a.out[o] : 0.f, acc_s = 0.f, acc_r = 0.f;
 #pragma unroll
         for (int q = 0; q < kMaxShared + kMaxTopk; q++) {  // q < S: shared expert q; else rank q - S
             if (q >= kq) continue;
+            const float y = __uint_as_float((unsigned)w[q]);
             if (q < S) {
-                if (q < a.n_shared) acc = acc + __uint_as_float((unsigned)w[q]);
+                if (q < a.n_shared) {
+                    acc = acc + y;
+                    acc_s = acc_s + y;
+                }
             } else if (q - S < a.keep && rt->id[t * k + q - S] >= 0) {
-                acc = fmaf(rt->gate[t * k + q - S], __uint_as_float((unsigned)w[q]), acc);
+                acc = fmaf(rt->gate[t * k + q - S], y, acc);
+                acc_r = fmaf(rt->gate[t * k + q - S], y, acc_r);
             }
         }
-        a.out[o] = acc;
+        combine_store(a, o, acc, acc_s, acc_r);
     }
 }
 
@@ -963,28 +1072,28 @@ struct SlotView {
 // ====================================================================================================================
 // Unfused path: one kernel per phase (stream order provides the dependencies; the tagged reads succeed at once).
 #if MOE_COMMON
-__global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T, const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T, StageSrc in,
                                                      uint64_t* __restrict__ logits, float* __restrict__ logits_out,
                                                      unsigned epoch) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
-    const int e0 = blockIdx.x * kWaves;
-    if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
-    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
-    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
-    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
-    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, x);
+    const int e0 = blockIdx.x * kRouterRows;
+    if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
+    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
+    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
+    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
+    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
 }
 
 __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
-                                                         int do_topk, const uint64_t* __restrict__ logits,
+                                                         int do_topk, int rule, const uint64_t* __restrict__ logits,
                                                          unsigned epoch, unsigned* err, int32_t* __restrict__ ids,
                                                          float* __restrict__ gates, Slots* __restrict__ slots) {
     __shared__ RouteTab rt_mem;
     __shared__ __align__(16) unsigned char scr_mem[kRouteScratchBytes];
     lds_RouteTab* rt = (lds_RouteTab*)&rt_mem;
     route_local(rt, (LDS_AS unsigned char*)scr_mem, logits, epoch, err, L.bias, ids, gates, T, d.E, d.k, keep, n_shared,
-                do_topk);
+                do_topk, rule, -1);
     route_publish(rt, T, d.k, keep, n_shared, do_topk, ids, gates, slots);
 }
 
@@ -1002,7 +1111,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     if (sl >= a.slots->nslot || (sl < a.d.n_shared && sl >= a.n_shared)) return;  // unused / left out
     SlotView<NT> v;
     v.load(a.slots, sl);
-    stage_x(s, a.x, a.T, a.d.H);
+    stage_in(s, a.in, a.T, a.d.H);
     uint64_t stamp = 0;
     gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, stamp);
 }
@@ -1104,30 +1213,48 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         if (blockIdx.x == 0) st_sync(&sy->next_unit[(ph ^ 1) * kSyncPad], 0u);  // the next launch's head
     }
     __syncthreads();
-    auto ensure_routed = [&]() {
-        if (!s_routed) {
-            route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
-                        a.d.E, a.d.k, a.keep, S, f.do_topk);
-            if (threadIdx.x == 0) s_routed = 1;
+    auto ensure_staged = [&]() __attribute__((always_inline)) {
+        if (!s_staged) {
+            stage_in(s, a.in, a.T, H);
+            if (threadIdx.x == 0) s_staged = 1;
             __syncthreads();
         }
     };
-    auto ensure_staged = [&]() {
-        if (!s_staged) {
-            stage_x(s, a.x, a.T, H);
-            if (threadIdx.x == 0) s_staged = 1;
+    auto ensure_routed = [&]() __attribute__((always_inline)) {
+        if (!s_routed) {
+            if (route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
+                            a.d.E, a.d.k, a.keep, S, f.do_topk, f.rule, f.do_topk ? f.router_poll : -1)) {
+                // Router logits still missing after the bounded wait: a router unit's workgroup is not running (the
+                // grid is not all resident).  Compute every router row here (the same bits: rewriting a logit that
+                // its unit also writes is harmless), then wait for them without a limit.
+                ensure_staged();
+                for (int r = 0; r < f.nR; r++)
+                    router_unit<NT>(s, a.L.wr, r * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, false, a.in);
+                __syncthreads();  // the router segments in s.as are route_local's scratch next
+                route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
+                            a.d.E, a.d.k, a.keep, S, f.do_topk, f.rule, -1);
+            }
+            if (threadIdx.x == 0) s_routed = 1;
             __syncthreads();
         }
     };
     uint64_t t_start = 0;
     int next = 0;  // thread 0: the unit after the current one
-    // Units b and grid + b are this workgroup's first two (no queue traffic while every workgroup starts at once);
-    // from the second unit on, the index after the current one is fetched from the queue while the current one runs.
-    const int grid = (int)gridDim.x;
-    for (int u = blockIdx.x, round = 0; u < uEnd; round++) {
+    // Every unit is handed out by the queue in ascending order, each to a workgroup that is running, except router
+    // unit b, which workgroup b (b < nS) runs first: a unit only waits for units of smaller index, and the smallest
+    // unfinished queue unit always has a running workgroup, so the grid needs no co-residency; a missing router unit
+    // is covered by ensure_routed.  The index after the current unit is fetched while the current one runs.
+    const int grid = (int)gridDim.x, nS = min(grid, f.nR);
+    auto claim = [&]() __attribute__((always_inline)) {
+        return nS + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if ((int)blockIdx.x >= nS) {
+        if (threadIdx.x == 0) s_unit = claim();
+        __syncthreads();
+    }
+    for (int u = (int)blockIdx.x < nS ? (int)blockIdx.x : __builtin_amdgcn_readfirstlane(s_unit); u < uEnd;) {
         if (threadIdx.x == 0) {
-            if (round == 0) next = grid + (int)blockIdx.x;
-            else next = 2 * grid + (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            next = claim();
             if (f.trace) t_start = __builtin_amdgcn_s_memrealtime();
         }
         const UnitRef ur = decode_unit(u, f.nR, S, maxs, gs, g, nht, f.lag, grid);
@@ -1135,8 +1262,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
-            router_unit<NT>(s, a.L.wr, ur.idx * kWaves, a.d.E, H, a.T, f.logits, nullptr, a.epoch,
-                            stage ? a.x : nullptr);
+            router_unit<NT>(s, a.L.wr, ur.idx * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, stage, a.in);
             if (stage && threadIdx.x == 0) s_staged = 1;
         } else if (ur.kind == 1) {
             ensure_routed();
@@ -1378,29 +1504,26 @@ __global__ void synth_fill_kernel(u32x4* __restrict__ dst, uint64_t nchunk, uint
 
 static inline unsigned nblk(size_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
-static hipError_t set_lds(const void* fn, size_t lds) {
-    if (lds <= 48 * 1024) return hipSuccess;
-    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-}
+static hipError_t set_lds(const void* fn, size_t lds) { return raise_lds_limit(fn, lds); }
 
 static int nt_bucket(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
 #if MOE_COMMON
-hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const uint16_t* x, uint64_t* logits,
+hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const StageSrc& in, uint64_t* logits,
                          float* logits_out, unsigned epoch, hipStream_t st) {
     const size_t lds = lds_bytes(T, 1, d.H, d.F, d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&router_kernel), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kWaves)), dim3(256), lds, st, L, d, T, x, logits, logits_out,
+    hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kRouterRows)), dim3(256), lds, st, L, d, T, in, logits, logits_out,
                        epoch);
     return hipGetLastError();
 }
 
-hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk,
+hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk, int rule,
                              const uint64_t* logits, unsigned epoch, unsigned* err, int32_t* ids, float* gates,
                              Slots* slots, hipStream_t st) {
-    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), 0, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, logits,
-                       epoch, err, ids, gates, slots);
+    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), 0, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, rule,
+                       logits, epoch, err, ids, gates, slots);
     return hipGetLastError();
 }
 
@@ -1426,12 +1549,12 @@ hipError_t down_nt(const ExpertArgs& ea, hipStream_t st) {
 }
 
 template <int NT>
-hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out);
+hipError_t fused_nt(FusedArgs f, int wg_per_cu, int grid_req, hipStream_t st, int* grid_out);
 #if defined(MOE_EXTERN_BUCKETS)
 #define MOE_BUCKET_DECL(N)                                                                         \
     extern template hipError_t gateup_nt<N>(const ExpertArgs&, Sync*, hipStream_t);                \
     extern template hipError_t down_nt<N>(const ExpertArgs&, hipStream_t);                         \
-    extern template hipError_t fused_nt<N>(FusedArgs, int, hipStream_t, int*);
+    extern template hipError_t fused_nt<N>(FusedArgs, int, int, hipStream_t, int*);
 MOE_BUCKET_DECL(1)
 MOE_BUCKET_DECL(2)
 MOE_BUCKET_DECL(4)
@@ -1467,7 +1590,7 @@ hipError_t launch_down(const ExpertArgs& ea, hipStream_t st) {
 #endif  // MOE_COMMON
 
 template <int NT>
-hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
+hipError_t fused_nt(FusedArgs f, int wg_per_cu, int grid_req, hipStream_t st, int* grid_out) {
     const void* fn = reinterpret_cast<const void*>(&fused_layer_kernel<NT>);
     const size_t lds = lds_bytes(f.e.T, NT, f.e.d.H, f.e.d.F, f.e.d.E);
     // occupancy per (device, LDS size), computed once: the launch itself stays a single host call
@@ -1476,8 +1599,8 @@ hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
     hipError_t e;
     int dev = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = set_lds(fn, lds)) != hipSuccess) return e;
     if (dev != c_dev || lds != c_lds) {
-        if ((e = set_lds(fn, lds)) != hipSuccess) return e;
         if ((e = hipDeviceGetAttribute(&c_ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
         if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&c_per_cu, fn, 256, lds)) != hipSuccess) return e;
         c_dev = dev;
@@ -1487,7 +1610,7 @@ hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
     if (wg_per_cu > 0 && wg_per_cu < per_cu) per_cu = wg_per_cu;
     if (per_cu < 1) return hipErrorInvalidConfiguration;
     const int units = fused_units(f.nR, f.e.maxs, f.e.d.n_shared, f.e.d.F, f.e.d.H, f.e.kp, f.e.kps);
-    int grid = ncu * per_cu;
+    int grid = grid_req > 0 ? grid_req : ncu * per_cu;  // a requested grid may exceed what fits at once
     if (grid > units) grid = units;
     if (grid_out) *grid_out = grid;
     hipLaunchKernelGGL(fused_layer_kernel<NT>, dim3(grid), dim3(256), lds, st, f);
@@ -1495,17 +1618,17 @@ hipError_t fused_nt(FusedArgs f, int wg_per_cu, hipStream_t st, int* grid_out) {
 }
 
 #if defined(MOE_PART) && MOE_PART > 0
-template hipError_t fused_nt<MOE_PART>(FusedArgs, int, hipStream_t, int*);
+template hipError_t fused_nt<MOE_PART>(FusedArgs, int, int, hipStream_t, int*);
 #endif
 
 #if MOE_COMMON
-hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, hipStream_t st, int* grid_out) {
+hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, int grid, hipStream_t st, int* grid_out) {
     switch (nt_bucket(f.e.T)) {
-        case 1: return fused_nt<1>(f, wg_per_cu, st, grid_out);
-        case 2: return fused_nt<2>(f, wg_per_cu, st, grid_out);
-        case 4: return fused_nt<4>(f, wg_per_cu, st, grid_out);
-        case 8: return fused_nt<8>(f, wg_per_cu, st, grid_out);
-        default: return fused_nt<16>(f, wg_per_cu, st, grid_out);
+        case 1: return fused_nt<1>(f, wg_per_cu, grid, st, grid_out);
+        case 2: return fused_nt<2>(f, wg_per_cu, grid, st, grid_out);
+        case 4: return fused_nt<4>(f, wg_per_cu, grid, st, grid_out);
+        case 8: return fused_nt<8>(f, wg_per_cu, grid, st, grid_out);
+        default: return fused_nt<16>(f, wg_per_cu, grid, st, grid_out);
     }
 }
 

@@ -38,13 +38,26 @@ SYMBOLS = (
     "moe_gpu_profile_kernels", "moe_gpu_profile_slots", "moe_gpu_profile_read", "moe_gpu_profile_reset",
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
-    "moe_rmsnorm_dev", "moe_gemv_dev", "moe_rope_dev", "moe_attn_workspace_bytes", "moe_attn_decode_dev",
-    "moe_attn_last_error",
+    "moe_rmsnorm_dev", "moe_gemv_dev", "moe_gemv_f32_dev", "moe_gemv_norm_dev", "moe_rope_dev", "moe_rope_append_dev",
+    "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
+    "moe_gpu_block_dev",
+    "moe_model_create", "moe_model_destroy", "moe_model_last_error", "moe_model_experts", "moe_model_head",
+    "moe_model_set_stream", "moe_model_synchronize", "moe_model_load_layer", "moe_model_load_embedding",
+    "moe_model_load_rope", "moe_model_set_layers", "moe_model_kv_cache", "moe_model_step_dev", "moe_model_step", "moe_model_residual",
 )
 ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
+OPT_GRID, OPT_ROUTER_POLL, OPT_ROUTE_RULE = 8, 9, 10
+ROUTE_SOFTMAX, ROUTE_SIGMOID = 0, 1
 
 _lib = None
+
+
+class ModelConfig(C.Structure):
+    """moe_model_config of include/moe_gpu.h."""
+    _fields_ = [(n, C.c_int) for n in ("H", "n_q_heads", "n_kv_heads", "head_dim", "F", "E", "topk", "n_shared",
+                                        "n_layers", "vocab", "max_ctx")] + \
+               [("eps", C.c_float), ("route_rule", C.c_int), ("argmax_rule", C.c_int)]
 
 
 class MoeGpuError(RuntimeError):
@@ -128,6 +141,25 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_attn_workspace_bytes": (C.c_size_t, [i, i, i]),
         "moe_attn_decode_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, C.c_size_t, vp]),
         "moe_attn_last_error": (C.c_char_p, []),
+        "moe_gemv_norm_dev": (i, [i, i, vp, vp, vp, f, vp, vp]),
+        "moe_gemv_f32_dev": (i, [i, i, vp, vp, vp, vp]),
+        "moe_rope_append_dev": (i, [i, i, i, vp, vp, vp, vp, vp, i, vp]),
+        "moe_gpu_block_dev": (i, [vp, i, i, vp, vp, vp, f, i, u, vp, vp, vp, vp]),
+        "moe_model_create": (i, [i, C.POINTER(ModelConfig), C.POINTER(vp)]),
+        "moe_model_destroy": (None, [vp]),
+        "moe_model_last_error": (C.c_char_p, [vp]),
+        "moe_model_experts": (vp, [vp]),
+        "moe_model_head": (vp, [vp]),
+        "moe_model_set_stream": (i, [vp, vp]),
+        "moe_model_synchronize": (i, [vp]),
+        "moe_model_load_layer": (i, [vp, i, vp, vp, vp, vp, vp, vp]),
+        "moe_model_load_embedding": (i, [vp, vp]),
+        "moe_model_load_rope": (i, [vp, vp, vp]),
+        "moe_model_kv_cache": (i, [vp, i, C.POINTER(vp), C.POINTER(vp)]),
+        "moe_model_set_layers": (i, [vp, i]),
+        "moe_model_step_dev": (i, [vp, vp, i, vp, vp]),
+        "moe_model_step": (i, [vp, i, i, C.POINTER(C.c_int32), C.POINTER(f)]),
+        "moe_model_residual": (i, [vp, vp]),
     }
     for name in SYMBOLS:
         fn = getattr(L, name)
@@ -359,6 +391,13 @@ class MoeGpu:
     def route_dev(self, layer: int, T: int, x, ids, gates, logits=None, keep: int = 0):
         self._chk(self.L.moe_gpu_route_dev(self.h, layer, T, _p(x), keep, _p(ids), _p(gates), _p(logits)))
 
+    def block_dev(self, layer: int, T: int, resid, attn_o, norm_w, x_next, eps: float = 1e-5, out=None, ids=None,
+                  gates=None, keep: int = 0, flags: int = 0):
+        """A decode layer's second half (main.rs:120-141): x_next = bf16(r + bf16(bf16(routed) + bf16(shared))) with
+        r = bf16(resid + attn_o) and the experts run on rmsnorm(r, norm_w).  Device tensors."""
+        self._chk(self.L.moe_gpu_block_dev(self.h, layer, T, _p(resid), _p(attn_o), _p(norm_w), eps, keep, flags,
+                                           _p(x_next), _p(out), _p(ids), _p(gates)))
+
 
 class LmHead:
     """The decode step's tail on the GPU: final RMSNorm, LM-head GEMV, greedy argmax (main.rs:381-386; the chip's
@@ -461,6 +500,106 @@ def attn_decode_dev(q, k_cache, v_cache, out, workspace, n_q_heads: int, n_kv_he
 
 def attn_workspace_bytes(n_q_heads: int, S: int, head_dim: int = 128) -> int:
     return int(load_library().moe_attn_workspace_bytes(n_q_heads, head_dim, S))
+
+
+def gemv_norm_dev(W, x, norm_w, y, eps: float = 1e-5, stream=None) -> None:
+    """y = bf16(W . rmsnorm(x, norm_w)) on device tensors (the input norm folded into the q|k|v projection)."""
+    M, K = W.shape
+    rc = load_library().moe_gemv_norm_dev(M, K, _p(W), _p(x), _p(norm_w), eps, _p(y),
+                                          getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, f"moe_gemv_norm_dev(M={M}, K={K}) failed")
+
+
+def rope_append_dev(qkv, cos_row, sin_row, k_cache, v_cache, pos: int, n_q_heads: int, n_kv_heads: int,
+                    head_dim: int = 128, stream=None) -> None:
+    rc = load_library().moe_rope_append_dev(n_q_heads, n_kv_heads, head_dim, _p(qkv), _p(cos_row), _p(sin_row),
+                                            _p(k_cache), _p(v_cache), pos, getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, "moe_rope_append_dev failed")
+
+
+class MoeModel:
+    """A whole MoE decoder's greedy decode step on one GPU (the engine's host step, main.rs:372-387).  The experts and
+    routers are loaded through ``experts`` (a MoeGpu view of the model's context), the LM head through ``head``."""
+
+    def __init__(self, H: int, n_q_heads: int, n_kv_heads: int, F: int, E: int, topk: int, n_shared: int,
+                 n_layers: int, vocab: int, max_ctx: int, eps: float = 1e-5, route_rule: int = ROUTE_SIGMOID,
+                 argmax_rule: int = ARGMAX_FP32, head_dim: int = 128, device: int = 0):
+        self.L = load_library()
+        cfg = ModelConfig(H, n_q_heads, n_kv_heads, head_dim, F, E, topk, n_shared, n_layers, vocab, max_ctx, eps,
+                          route_rule, argmax_rule)
+        h = C.c_void_p()
+        rc = self.L.moe_model_create(device, C.byref(cfg), C.byref(h))
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_model_last_error(None).decode())
+        self.h, self.cfg = h, cfg
+        self.experts = MoeGpu.__new__(MoeGpu)  # a view: the model owns and destroys the context
+        self.experts.L, self.experts.h = self.L, C.c_void_p(self.L.moe_model_experts(h))
+        self.experts.H, self.experts.F, self.experts.E, self.experts.k = H, F, E, topk
+        self.experts.n_shared, self.experts.n_layers, self.experts.max_tokens = n_shared, n_layers, 1
+        self.experts.close = lambda: None
+        self.head = LmHead.__new__(LmHead)
+        self.head.L, self.head.h, self.head.H, self.head.V = self.L, C.c_void_p(self.L.moe_model_head(h)), H, vocab
+        self.head.close = lambda: None
+
+    def _chk(self, rc: int):
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_model_last_error(self.h).decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.moe_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream) -> None:
+        self._chk(self.L.moe_model_set_stream(self.h, getattr(stream, "cuda_stream", stream)))
+
+    def synchronize(self):
+        self._chk(self.L.moe_model_synchronize(self.h))
+
+    def load_layer(self, layer: int, in_norm, wq, wk, wv, wo, post_norm):
+        """Host arrays (uint16 bf16 bits) or device tensors."""
+        arrs = [a if hasattr(a, "data_ptr") else _u16(a) for a in (in_norm, wq, wk, wv, wo, post_norm)]
+        self._chk(self.L.moe_model_load_layer(self.h, layer, *[_p(a) for a in arrs]))
+
+    def load_embedding(self, emb):
+        emb = emb if hasattr(emb, "data_ptr") else _u16(emb)
+        self._chk(self.L.moe_model_load_embedding(self.h, _p(emb)))
+
+    def load_rope(self, cos_tab, sin_tab):
+        c = cos_tab if hasattr(cos_tab, "data_ptr") else _u16(cos_tab)
+        s_ = sin_tab if hasattr(sin_tab, "data_ptr") else _u16(sin_tab)
+        self._chk(self.L.moe_model_load_rope(self.h, _p(c), _p(s_)))
+
+    def set_layers(self, n: int):
+        """Steps run the first n layers, then the head."""
+        self._chk(self.L.moe_model_set_layers(self.h, n))
+
+    def kv_cache(self, layer: int):
+        """(k, v) device addresses of the layer's caches [max_ctx, NKV, D] bf16."""
+        k, v = C.c_void_p(), C.c_void_p()
+        self._chk(self.L.moe_model_kv_cache(self.h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def step(self, token: int, pos: int):
+        nxt, best = C.c_int32(), C.c_float()
+        self._chk(self.L.moe_model_step(self.h, token, pos, C.byref(nxt), C.byref(best)))
+        return int(nxt.value), float(best.value)
+
+    def step_dev(self, token, pos: int, nxt, best=None):
+        self._chk(self.L.moe_model_step_dev(self.h, _p(token), pos, _p(nxt), _p(best)))
+
+    def residual(self) -> np.ndarray:
+        x = np.zeros(self.cfg.H, np.uint16)
+        self._chk(self.L.moe_model_residual(self.h, _p(x)))
+        return x
 
 
 def gpu_moe(tier: MoeGpu, layer: int, x, experts: Sequence[int], toks: Sequence, ws: Sequence) -> np.ndarray:

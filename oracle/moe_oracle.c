@@ -14,6 +14,7 @@
  *   - quant_row ....................... track2_opt/solar_engine/csrc/cpu_kern.c:218-224
  *   - ck_moe_q8w (int8 weight-only) ... track2_opt/solar_engine/csrc/cpu_kern.c:291-333
  *   - softmax route() ................. npu-kernels/npu_kernels/rngd/layer_template/src/host.rs.tpl:247-267
+ *   - sigmoid route() (Solar) ......... track2_opt/solar_engine/src/host.rs:119-128
  *   - expert grouping (first seen) .... solar_hybrid/runtime.py:344-354
  *
  * The scalar dot products emulate the exact arithmetic of the reference's AVX-512 code: 16 fp32 lanes, each lane
@@ -21,9 +22,7 @@
  * FTZ output, RNE), two accumulators over 64-element steps, then GCC's _mm512_reduce_add_ps tree.  They therefore
  * reproduce the reference's fp32 bits, which the tests check against the reference's own compiled cpu_kern.c.
  *
- * The router-logit function or_router_logits_wave() restates a different, documented order: the one the HIP router
- * kernel uses (64 lanes, strided 8-element chunks, sequential fma per lane, xor-butterfly).  Its only purpose is to
- * make the GPU's logits — and therefore its top-k selection — checkable bit-for-bit.
+ * The HIP router kernel computes its logits in ck_gemv's own order, so or_gemv() is also the GPU logits' mirror.
  *
  * The AVX-512 CPU-baseline port of cpu_moe lives in cpu_moe_port.c (its own library, AVX-512 flags).
  */
@@ -200,31 +199,6 @@ OR_API void or_moe_q8w(int E, const int8_t* const* q, const float* const* sc, co
     free(g); free(act);
 }
 
-/* ------------------------------------------------------------------ router logits, GPU wave order
- * logits[t,e] = sum_h x[t,h] * wr[e,h] computed exactly as the HIP router kernel does:
- *   lane l in 0..63 owns 8-element chunks c = l + 64*j (j = 0 .. H/512-1); per lane a sequential fused
- *   multiply-add chain over (j ascending, element 0..7 ascending); then a 64-lane xor butterfly
- *   (offsets 32,16,8,4,2,1), each step v = v + v[lane ^ offset].  Requires H % 512 == 0. */
-OR_API void or_router_logits_wave(int T, int E, int H, const uint16_t* x, const uint16_t* wr, float* logits) {
-    float v[64], nv[64];
-    for (int t = 0; t < T; t++)
-        for (int e = 0; e < E; e++) {
-            const uint16_t* row = wr + (size_t)e * H;
-            const uint16_t* xt = x + (size_t)t * H;
-            for (int l = 0; l < 64; l++) {
-                float acc = 0.f;
-                for (int c = l; c < H / 8; c += 64)
-                    for (int i = 0; i < 8; i++) acc = fmaf(or_bf2f(row[c * 8 + i]), or_bf2f(xt[c * 8 + i]), acc);
-                v[l] = acc;
-            }
-            for (int m = 32; m >= 1; m >>= 1) {
-                for (int l = 0; l < 64; l++) nv[l] = v[l] + v[l ^ m];
-                memcpy(v, nv, sizeof v);
-            }
-            logits[(size_t)t * E + e] = v[0];
-        }
-}
-
 /* ------------------------------------------------------------------ softmax route (host.rs.tpl:247-267)
  * Per token: score = logits (+ bias, added to the logits: the bias is a routing prior on the logit scale);
  * s = softmax(score) over all E; select the k largest scores, stable with ties to the lower index;
@@ -258,6 +232,39 @@ OR_API void or_route_softmax(int T, int E, int k, int keep, const float* logits,
         }
     }
     free(sc); free(s); free(idx);
+}
+
+/* ------------------------------------------------------------------ sigmoid route (host.rs:119-128)
+ * Solar's route(): s = 1 / (1 + exp(-logit)) in fp32 (exp is the C library's expf, the function Rust's f32::exp
+ * calls); the k largest s + bias are selected by a stable descending sort (ties keep the lower index); the gates are
+ * the unbiased s of the selected ranks over (their sequential sum + 1e-20).  keep < k (this build's rank drop) sums
+ * and keeps only the first keep ranks. */
+OR_API void or_route_sigmoid(int T, int E, int k, int keep, const float* logits, const float* bias, int32_t* ids,
+                             float* gates) {
+    float* s = (float*)malloc(sizeof(float) * E);
+    float* key = (float*)malloc(sizeof(float) * E);
+    int* idx = (int*)malloc(sizeof(int) * E);
+    if (keep <= 0 || keep > k) keep = k;
+    for (int t = 0; t < T; t++) {
+        const float* lg = logits + (size_t)t * E;
+        for (int e = 0; e < E; e++) {
+            s[e] = 1.0f / (1.0f + expf(-lg[e]));
+            key[e] = bias ? s[e] + bias[e] : s[e];
+        }
+        for (int e = 0; e < E; e++) {
+            int p = e;
+            while (p > 0 && key[idx[p - 1]] < key[e]) { idx[p] = idx[p - 1]; p--; }
+            idx[p] = e;
+        }
+        float tot = 0.f;
+        for (int j = 0; j < keep; j++) tot += s[idx[j]];
+        tot += 1e-20f;
+        for (int j = 0; j < k; j++) {
+            ids[(size_t)t * k + j] = idx[j];
+            gates[(size_t)t * k + j] = j < keep ? s[idx[j]] / tot : 0.f;
+        }
+    }
+    free(s); free(key); free(idx);
 }
 
 /* ------------------------------------------------------------------ layer combine (fixed order)

@@ -11,7 +11,7 @@ three libraries built by ``oracle/Makefile``:
 
 Function names follow the reference: ``cpu_moe`` (cpu_moe.cpp:38), ``ck_moe3`` (cpu_kern.c:141), ``gemv``
 (cpu_kern.c:32), ``quant_row``/``quant_expert`` (cpu_kern.c:218, :227), ``moe_q8w`` (cpu_kern.c:306), ``route``
-(host.rs.tpl:247), ``group_tokens`` (runtime.py:344-347), ``rmsnorm`` (host.rs:71-76), ``lm_head_argmax``
+(host.rs.tpl:247 softmax, host.rs:119 sigmoid), ``group_tokens`` (runtime.py:344-347), ``rmsnorm`` (host.rs:71-76), ``lm_head_argmax``
 (main.rs:384-385, chip.rs:183-194), ``attention`` (main.rs:86-104), ``rope`` (main.rs:65-77).
 """
 from __future__ import annotations
@@ -58,10 +58,9 @@ def lib() -> C.CDLL:
         L.or_quant_expert.argtypes = [u16p, u16p, u16p, i8p, f32p, i32p, C.c_int, C.c_int]
         L.or_moe_q8w.restype = None
         L.or_moe_q8w.argtypes = [C.c_int, C.c_void_p, C.c_void_p, f32p, u16p, f32p, C.c_int, C.c_int]
-        L.or_router_logits_wave.restype = None
-        L.or_router_logits_wave.argtypes = [C.c_int, C.c_int, C.c_int, u16p, u16p, f32p]
-        L.or_route_softmax.restype = None
-        L.or_route_softmax.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, f32p, C.c_void_p, i32p, f32p]
+        for fn in (L.or_route_softmax, L.or_route_sigmoid):
+            fn.restype = None
+            fn.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, f32p, C.c_void_p, i32p, f32p]
         L.or_combine.restype = None
         L.or_combine.argtypes = [C.c_int] * 5 + [f32p, f32p, i32p, f32p, f32p, C.c_int]
         L.or_synth_key.restype = C.c_uint64; L.or_synth_key.argtypes = [C.c_uint64, C.c_uint64]
@@ -157,23 +156,21 @@ def moe_q8w(qs, scs, w, x, out, H, F) -> None:
                      np.ascontiguousarray(x, np.uint16), out, H, F)
 
 
-def router_logits_wave(x: np.ndarray, wr: np.ndarray) -> np.ndarray:
-    """Router logits in the HIP router kernel's documented order (bit-exact mirror): [T,E] fp32."""
-    x = np.ascontiguousarray(x, np.uint16); wr = np.ascontiguousarray(wr, np.uint16)
-    T, H = x.shape; E = wr.shape[0]
-    assert H % 512 == 0
-    out = np.zeros((T, E), np.float32)
-    lib().or_router_logits_wave(T, E, H, x, wr, out)
-    return out
+def router_logits(x: np.ndarray, wr: np.ndarray) -> np.ndarray:
+    """Router logits [T,E] fp32: ck_gemv (cpu_kern.c:31-35) of the router weight for every token row."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.uint16)
+    return np.stack([gemv(wr, x[t]) for t in range(x.shape[0])])
 
 
-def route(logits: np.ndarray, bias: np.ndarray | None, k: int, keep: int | None = None):
-    """softmax route (host.rs.tpl:247-267) on (logits + bias): ids [T,k] int32, gates [T,k] fp32 (ranks >= keep: 0)."""
+def route(logits: np.ndarray, bias: np.ndarray | None, k: int, keep: int | None = None, rule: str = "softmax"):
+    """ids [T,k] int32, gates [T,k] fp32 (ranks >= keep: 0).  rule "softmax": host.rs.tpl:247-267 on (logits + bias);
+    rule "sigmoid": Solar's route(), host.rs:119-128 (sigmoid scores, the bias selects only, gates s / (sum + 1e-20))."""
     logits = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
     T, E = logits.shape
     ids = np.zeros((T, k), np.int32); gates = np.zeros((T, k), np.float32)
     b = np.ascontiguousarray(bias, np.float32) if bias is not None else None
-    lib().or_route_softmax(T, E, k, keep or k, logits, b.ctypes.data if b is not None else None, ids, gates)
+    fn = {"softmax": lib().or_route_softmax, "sigmoid": lib().or_route_sigmoid}[rule]
+    fn(T, E, k, keep or k, logits, b.ctypes.data if b is not None else None, ids, gates)
     return ids, gates
 
 

@@ -1,8 +1,9 @@
 """Test helpers: host-side weight generation and the oracle's view of one MoE layer call.
 
-The oracle composes the restated reference kernels (oracle/moe_oracle.c): router logits in the GPU's documented order,
-softmax top-k route (host.rs.tpl:247-267), per-expert outputs with cpu_moe semantics (cpu_moe.cpp:38-96) or
-ck_moe_q8w semantics for int8 (cpu_kern.c:306-333), and the fixed-order combine.
+The oracle composes the restated reference kernels (oracle/moe_oracle.c): router logits by ck_gemv (cpu_kern.c:31-35,
+the order the GPU router also uses), the softmax (host.rs.tpl:247-267) or sigmoid (host.rs:119-128) top-k route,
+per-expert outputs with cpu_moe semantics (cpu_moe.cpp:38-96) or ck_moe_q8w semantics for int8 (cpu_kern.c:306-333),
+and the fixed-order combine.
 """
 from __future__ import annotations
 
@@ -28,6 +29,23 @@ def assert_layer_close(got, exp, max_abs=2e-2, rel_l2=5e-3):
     r = tolerance_report(got, exp)
     assert r["finite"], r
     assert r["max_abs"] <= max_abs and r["rel_l2"] <= rel_l2, r
+    return r
+
+
+def assert_bf16_close(got: np.ndarray, exp: np.ndarray, max_ulp: int = 2, rel_l2: float = 1e-2):
+    """bf16 values (bit arrays) that went through several roundings in different summation orders: each element within
+    max_ulp bf16 ulps, an ulp taken at the larger of the element's magnitude and the reference's rms (a value near zero
+    is the sum of terms of ordinary size, so its error is one of ordinary size), and rel-L2 within rel_l2."""
+    g = O.bf2f(got).astype(np.float64); e = O.bf2f(exp).astype(np.float64)
+    assert np.isfinite(g).all()
+    rms = float(np.sqrt(np.mean(e * e))) if e.size else 0.0
+    mag = np.maximum(np.maximum(np.abs(g), np.abs(e)), rms)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 2.0 ** -126))) - 7)
+    d = np.abs(g - e)
+    worst = float((d / ulp).max()) if d.size else 0.0
+    r = {"max_ulp": worst, "rel_l2": float(np.linalg.norm(g - e) / max(np.linalg.norm(e), 1e-30)),
+         "frac_diff": float((d > 0).mean())}
+    assert worst <= max_ulp and r["rel_l2"] <= rel_l2, r
     return r
 
 
@@ -104,7 +122,8 @@ def random_x(T: int, H: int, rng: np.random.Generator) -> np.ndarray:
 
 # ------------------------------------------------------------------------------------------ oracle layer
 def oracle_layer(hl: HostLayer, x: np.ndarray, keep: int | None = None, int8: bool | None = None,
-                 ids: np.ndarray | None = None, gates: np.ndarray | None = None, with_shared: bool = True):
+                 ids: np.ndarray | None = None, gates: np.ndarray | None = None, with_shared: bool = True,
+                 rule: str = "softmax"):
     """Returns dict(logits, ids, gates, out) for one layer call on x [T,H]."""
     w = hl.w
     x = np.atleast_2d(x)
@@ -113,8 +132,8 @@ def oracle_layer(hl: HostLayer, x: np.ndarray, keep: int | None = None, int8: bo
     q8 = w.int8 if int8 is None else int8
     logits = None
     if ids is None:
-        logits = O.router_logits_wave(x, hl.router())
-        ids, gates = O.route(logits, hl.bias, w.k, keep)
+        logits = O.router_logits(x, hl.router())
+        ids, gates = O.route(logits, hl.bias, w.k, keep, rule=rule)
     nsh = w.n_shared if with_shared else 0
     ysh = np.zeros((T, nsh, w.H), np.float32)
     yr = np.zeros((T, w.k, w.H), np.float32)
@@ -134,3 +153,59 @@ def oracle_layer(hl: HostLayer, x: np.ndarray, keep: int | None = None, int8: bo
                 yr[t, r] = O.expert_y(x[t], np.concatenate([g, u]), d)
     out = O.combine(ysh, yr, ids, gates, keep)
     return {"logits": logits, "ids": ids, "gates": gates, "out": out, "ysh": ysh, "yr": yr, "keep": keep}
+
+
+# ------------------------------------------------------------------------------------------ decode step oracle
+def oracle_moe_block(hl: HostLayer, r: np.ndarray, post_norm: np.ndarray, rule: str = "sigmoid"):
+    """A decode layer's MoE half as the reference's host layer computes it (track2_opt/solar_engine/src/main.rs:
+    121-141): h2 = rmsnorm(r, post_attention_layernorm); logits = ck_gemv(router, h2); route; the shared expert(s)
+    summed (gate 1.0) and rounded to bf16; the routed experts' gated sum (one fused multiply-add per rank, rank
+    order) rounded to bf16; x = bf16(r + bf16(moe + shared)).  r: bf16 bits [H].  Returns (x bits, ids, score margin
+    between the k-th and (k+1)-th selection key)."""
+    w = hl.w
+    h2 = O.rmsnorm(r, post_norm)
+    lg = O.gemv(hl.router(), h2)
+    ids, gates = O.route(lg[None], hl.bias, w.k, None, rule=rule)
+    s = (np.float32(1) / (np.float32(1) + np.exp(-lg).astype(np.float32))) if rule == "sigmoid" else lg
+    key = np.sort((s + (hl.bias if hl.bias is not None else 0)).astype(np.float32))[::-1]
+    margin = float(key[w.k - 1] - key[w.k])
+    shared = np.zeros(w.H, np.float32)
+    for si in range(w.n_shared):
+        g, u, d = hl.shared(si)
+        shared = (shared + O.expert_y(h2, np.concatenate([g, u]), d)).astype(np.float32)
+    yr = np.zeros((1, w.k, w.H), np.float32)
+    for rk in range(w.k):
+        g, u, d = hl.expert(int(ids[0, rk]))
+        yr[0, rk] = O.expert_y(h2, np.concatenate([g, u]), d)
+    moe = O.combine(np.zeros((1, 0, w.H), np.float32), yr, ids, gates, w.k)[0]  # fma chain from 0, rank order
+    m = O.bf2f(O.f2bf(O.bf2f(O.f2bf(moe)) + O.bf2f(O.f2bf(shared))))
+    x = O.f2bf(O.bf2f(r) + m)
+    return x, ids[0], margin
+
+
+def oracle_decode_layer(x: np.ndarray, lw: dict, kc: np.ndarray, vc: np.ndarray, pos: int, cos_row: np.ndarray,
+                        sin_row: np.ndarray, hl: HostLayer, n_q: int, n_kv: int, rule: str = "sigmoid"):
+    """One decoder layer of the reference's host step (main.rs:106-126): input norm, q/k/v GEMV + round_bf, RoPE,
+    KV append at pos (kc / vc [max_ctx, NKV, D] updated in place), attention over 0..pos, o GEMV + round_bf, then the
+    MoE half.  x: bf16 bits [H].  Returns (x bits, ids, routing margin)."""
+    D = 128
+    h = O.rmsnorm(x, lw["in_norm"])
+    q = O.f2bf(O.gemv(lw["wq"], h)).reshape(n_q, D)
+    k = O.f2bf(O.gemv(lw["wk"], h)).reshape(n_kv, D)
+    v = O.f2bf(O.gemv(lw["wv"], h)).reshape(n_kv, D)
+    q = O.rope(q, cos_row, sin_row)
+    kc[pos] = O.rope(k, cos_row, sin_row)
+    vc[pos] = v
+    a, _ = O.attention(q, kc[:pos + 1], vc[:pos + 1], n_kv)
+    o = O.f2bf(O.gemv(lw["wo"], a.ravel()))
+    r = O.f2bf(O.bf2f(x) + O.bf2f(o))
+    return oracle_moe_block(hl, r, lw["post_norm"], rule)
+
+
+def rope_tables(max_ctx: int, D: int = 128, theta: float = 1e6):
+    """cos / sin rows [max_ctx, D] as bf16 bits in HF layout (the D/2 frequencies repeated for both halves), the
+    format of the reference's rope_cos.bin / rope_sin.bin (main.rs:4)."""
+    inv = theta ** (-np.arange(0, D, 2, dtype=np.float64) / D)
+    ang = np.arange(max_ctx, dtype=np.float64)[:, None] * inv[None, :]
+    ang = np.concatenate([ang, ang], axis=1)
+    return O.f2bf(np.cos(ang).astype(np.float32)), O.f2bf(np.sin(ang).astype(np.float32))

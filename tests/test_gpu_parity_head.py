@@ -113,6 +113,42 @@ def test_constructed_ties_and_rules():
         head.close()
 
 
+def test_signed_zero_and_nan_rules():
+    """Mixed-sign zeros tie (the lower row wins) and a NaN is never picked, except a NaN at row 0 under the fp32 rule,
+    which the reference's first-maximum loop (main.rs:384-385: `lg[i] > lg[best]` from best = 0) never leaves.
+    w_final = 2^-70 e0 makes logit[v] = W[v, 0] * 2^-70: W[5, 0] = -2^-70 gives -2^-140, which rounds to bf16 -0;
+    W[9, 0] = +2^-70 gives bf16 +0; every other row is -2^-70 (bf16-exact), so under the bf16 rule rows 5 and 9 tie at
+    zero (chip.rs:183-194: equal values -> lower row)."""
+    H, V = 1024, 64
+    W = np.zeros((V, H), np.uint16)
+    W[:, 0] = bf(-1.0)
+    W[5, 0] = bf(-(2.0 ** -70))
+    W[9, 0] = bf(2.0 ** -70)
+    wf = np.zeros(H, np.uint16)
+    wf[0] = bf(2.0 ** -70)
+    x = np.full((1, H), bf(1.0), np.uint16)
+    head = LmHead(H, V)
+    try:
+        say("signed zeros: bf16 rule ties -0 and +0")
+        head.load(W, wf)
+        ids, best = head.argmax(x, rule=ARGMAX_BF16)
+        assert ids.tolist() == [5] and best.tolist() == [0.0]
+        say("NaN rows: never picked, except row 0 under the fp32 rule")
+        W[3, 0] = 0x7FC0  # NaN
+        head.load(W, wf)
+        for rule in (ARGMAX_FP32, ARGMAX_BF16):
+            ids, _ = head.argmax(x, rule=rule)
+            assert int(ids[0]) in (5, 9) and (rule == ARGMAX_FP32 or int(ids[0]) == 5)
+        W[0, 0] = 0x7FC0
+        head.load(W, wf)
+        ids, best = head.argmax(x, rule=ARGMAX_FP32)
+        assert ids.tolist() == [0] and np.isnan(best[0])
+        ids, _ = head.argmax(x, rule=ARGMAX_BF16)
+        assert ids.tolist() == [5]
+    finally:
+        head.close()
+
+
 def test_head_errors():
     head = LmHead(1024, 64)
     try:

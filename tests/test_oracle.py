@@ -142,7 +142,7 @@ def test_dot_exact_on_small_integers():
     x = bf(rng.integers(-4, 5, (2, 512)))
     wr = bf(rng.integers(-4, 5, (5, 512)))
     exact = (O.bf2f(x).astype(np.int64) @ O.bf2f(wr).astype(np.int64).T).astype(np.float32)
-    np.testing.assert_array_equal(O.router_logits_wave(x, wr), exact)
+    np.testing.assert_array_equal(O.router_logits(x, wr), exact)
 
 
 def test_cpu_moe_matches_float64_closed_form():
@@ -279,17 +279,51 @@ def test_route_matches_stable_argsort_with_bias():
     assert (bias[ids].mean() > bias.mean())                               # the prior skews selection to hot experts
 
 
-def test_router_logits_wave_close_to_float64_and_to_ck_gemv_order():
+def test_router_logits_close_to_float64():
     rng = np.random.default_rng(12)
     x = bf(rng.normal(0, 1, (3, 1024))); wr = bf(rng.normal(0, 0.02, (16, 1024)))
-    lg = O.router_logits_wave(x, wr)
+    lg = O.router_logits(x, wr)
     ref = O.bf2f(x).astype(np.float64) @ O.bf2f(wr).astype(np.float64).T
     bound = 1e-6 * (np.abs(O.bf2f(x)).astype(np.float64) @ np.abs(O.bf2f(wr)).astype(np.float64).T)
     assert np.all(np.abs(lg - ref) <= bound)
-    for t in range(3):
-        ck = O.gemv(wr, x[t])  # the reference's ck_gemv order
-        assert np.abs(ck - lg[t]).max() < 1e-5
-        assert O.route(ck[None], None, 2)[0].tolist() == O.route(lg[t:t + 1], None, 2)[0].tolist()
+
+
+def test_sigmoid_route_hand_cases():
+    """Solar's route() (host.rs:119-128): selection by sigmoid(logit) + bias, ties to the lower index, gates are the
+    unbiased sigmoids over (their sum + 1e-20)."""
+    lg = np.array([[0.0, 2.0, 2.0, -1.0, 2.0, 0.5, 1.0, 1.0]], np.float32)
+    ids, gates = O.route(lg, None, 4, rule="sigmoid")
+    assert ids.tolist() == [[1, 2, 4, 6]]                                 # three-way tie of 2.0 -> 1, 2, 4; then 6 < 7
+    s = 1.0 / (1.0 + np.exp(-lg[0].astype(np.float64)))
+    sel = s[[1, 2, 4, 6]]
+    assert np.abs(gates[0] - sel / (sel.sum() + 1e-20)).max() < 1e-7
+    # the bias moves the selection but not the gates: expert 3 (logit -1) lifted above everything
+    bias = np.zeros(8, np.float32); bias[3] = 1.0
+    ids_b, gates_b = O.route(lg, bias, 4, rule="sigmoid")
+    assert ids_b.tolist() == [[3, 1, 2, 4]]
+    sel_b = s[[3, 1, 2, 4]]
+    assert np.abs(gates_b[0] - sel_b / (sel_b.sum() + 1e-20)).max() < 1e-7
+    # rank drop: keep 2 renormalises over the first two
+    ids_k, gates_k = O.route(lg, None, 4, keep=2, rule="sigmoid")
+    assert ids_k.tolist() == ids.tolist() and not gates_k[0, 2:].any()
+    assert abs(float(gates_k[0, 0]) - 0.5) < 1e-7
+    # an all-minus-infinity row: every s is 0, the 1e-20 keeps the gates finite (0)
+    ids_z, gates_z = O.route(np.full((1, 8), -np.inf, np.float32), None, 2, rule="sigmoid")
+    assert ids_z.tolist() == [[0, 1]] and not gates_z.any()
+
+
+def test_sigmoid_route_matches_float64_argsort_with_bias():
+    rng = np.random.default_rng(13)
+    E, k = 128, 8
+    bias = (rng.normal(0, 0.05, E)).astype(np.float32)
+    lg = rng.normal(0, 1.3, (64, E)).astype(np.float32)
+    ids, gates = O.route(lg, bias, k, rule="sigmoid")
+    for t in range(64):
+        s32 = (np.float32(1.0) / (np.float32(1.0) + np.exp(-lg[t]).astype(np.float32))).astype(np.float32)
+        ref = np.argsort(-(s32 + bias), kind="stable")[:k]
+        assert ids[t].tolist() == ref.tolist()
+        s64 = 1.0 / (1.0 + np.exp(-lg[t, ref].astype(np.float64)))
+        assert np.abs(gates[t] - s64 / s64.sum()).max() < 1e-6
 
 
 def test_group_tokens_first_seen_order():
