@@ -261,6 +261,17 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
                         size_t workspace_bytes, void* stream);
 const char* moe_attn_last_error(void); /* message of this thread's last failed moe_attn_decode_dev */
 
+/* Allocation-free variant of moe_attn_decode_dev.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * scores and partials live in a file-scope device array of moe_attn_noalloc_max_bytes() bytes (4 MiB: 64 query heads
+ * x 8192 positions), one per GPU, held until the process ends; its address is looked up once per device.  The call
+ * allocates nothing; it returns MOE_GPU_EINVAL, enqueueing nothing, when moe_attn_workspace_bytes(n_q_heads,
+ * head_dim, S) exceeds that size.  Outputs are bit-identical to moe_attn_decode_dev's.  All calls on one GPU share
+ * its array: calls that overlap on one GPU (two streams, two threads) race; serialise them on one stream. */
+size_t moe_attn_noalloc_max_bytes(void);
+int moe_attn_decode_noalloc_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                                const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* stream);
+
 /* ----------------------------------------------------------------------------------------------- decode step
  * One greedy decode step of a whole MoE decoder, replacing the engine's host step (track2_opt/solar_engine/src/
  * main.rs:372-387 `step`, with `layer` :106-126 and `moe_host` :128-141): x = embedding[token]; per layer the

@@ -11,6 +11,8 @@
 
 #include <stddef.h>
 
+#include <mutex>
+
 #include "moe_gpu.h"
 
 namespace {
@@ -283,6 +285,36 @@ int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale,
     return MOE_GPU_OK;
 }
 
+// The allocation-free entry point's scratch: the scores and partials of one call, for up to kScratchMaxNQ query
+// heads and kScratchMaxS positions (4 MiB per GPU, held until the process ends).  Host code never uses the array's
+// name as an address: the device address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and kept in g_scratch.
+constexpr int kScratchMaxNQ = 64, kScratchMaxS = 8192;
+constexpr size_t kScratchBytes =
+    (size_t)kScratchMaxNQ * kScratchMaxS * sizeof(float) +
+    (size_t)kScratchMaxNQ * ((kScratchMaxS + kChunk - 1) / kChunk) * kD * sizeof(float);
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_of_current_device(void** ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return afail(MOE_GPU_EHIP, "hipGetDevice failed");
+    if (dev < 0 || dev >= kMaxDevices) return afail(MOE_GPU_EINVAL, "device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return afail(e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP,
+                         "hipGetSymbolAddress(scratch) failed");
+        g_scratch[dev] = p;
+    }
+    *ptr = g_scratch[dev];
+    return MOE_GPU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -292,6 +324,20 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
                         size_t workspace_bytes, void* stream) {
     return attn_launch(n_q_heads, n_kv_heads, head_dim, S, scale, q, k_cache, v_cache, out, workspace, workspace_bytes,
                        stream);
+}
+
+size_t moe_attn_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int moe_attn_decode_noalloc_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                                const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* stream) {
+    const size_t need = moe_attn_workspace_bytes(n_q_heads, head_dim, S);
+    if (need == 0) return afail(MOE_GPU_EINVAL, "bad n_q_heads / head_dim / S");
+    if (need > kScratchBytes)
+        return afail(MOE_GPU_EINVAL, "n_q_heads * S beyond the allocation-free scratch (moe_attn_noalloc_max_bytes)");
+    void* ws = nullptr;
+    const int rc = scratch_of_current_device(&ws);
+    if (rc != MOE_GPU_OK) return rc;
+    return attn_launch(n_q_heads, n_kv_heads, head_dim, S, scale, q, k_cache, v_cache, out, ws, kScratchBytes, stream);
 }
 
 }  // extern "C"

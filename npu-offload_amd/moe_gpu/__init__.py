@@ -39,7 +39,8 @@ SYMBOLS = (
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
     "moe_rmsnorm_dev", "moe_gemv_dev", "moe_gemv_f32_dev", "moe_gemv_norm_dev", "moe_rope_dev", "moe_rope_append_dev",
-    "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error",
+    "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error", "moe_attn_noalloc_max_bytes",
+    "moe_attn_decode_noalloc_dev",
     "moe_gpu_block_dev",
     "moe_model_create", "moe_model_destroy", "moe_model_last_error", "moe_model_experts", "moe_model_head",
     "moe_model_set_stream", "moe_model_synchronize", "moe_model_load_layer", "moe_model_load_embedding",
@@ -141,6 +142,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_attn_workspace_bytes": (C.c_size_t, [i, i, i]),
         "moe_attn_decode_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, C.c_size_t, vp]),
         "moe_attn_last_error": (C.c_char_p, []),
+        "moe_attn_noalloc_max_bytes": (C.c_size_t, []),
+        "moe_attn_decode_noalloc_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp]),
         "moe_gemv_norm_dev": (i, [i, i, vp, vp, vp, f, vp, vp]),
         "moe_gemv_f32_dev": (i, [i, i, vp, vp, vp, vp]),
         "moe_rope_append_dev": (i, [i, i, i, vp, vp, vp, vp, vp, i, vp]),
