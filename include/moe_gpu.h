@@ -178,7 +178,8 @@ int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
  * {start, inputs ready, end, workgroup, aux, aux2} in the 100 MHz s_memrealtime clock.  Inputs ready: a routed gate|up
  * part's routing known, a combining down unit's other terms in, else 0; aux: a gate|up tile's finishing part has its
- * sibling parts' sums, a down unit its act rows, else 0; aux2: a down unit's weight stream done, else 0.  read_trace
+ * sibling parts' sums, a down unit its act rows, a router unit its operands, else 0; aux2: a down unit's weight stream
+ * done, a router unit's dot products done, else 0.  read_trace
  * copies the last launch's records (6 uint64 per unit, in the fused kernel's unit order). */
 int moe_gpu_trace_units(moe_gpu* ctx, int on);
 int moe_gpu_read_trace(moe_gpu* ctx, uint64_t* buf, int max_units, int* units);

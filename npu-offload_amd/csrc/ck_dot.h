@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace moe {
 
 namespace ckdot {
@@ -73,6 +75,125 @@ __device__ __forceinline__ void ck_row_dot(const ckdot::v4u* __restrict__ row, i
                 }
                 __builtin_amdgcn_wave_barrier();
             }
+        }
+    }
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t] = acc[t] + __shfl_xor(acc[t], m, 64);
+    }
+}
+
+// The router table in chain order: row e's dword k = 32 s + c (step s, chain c) sits at dword
+// 4 (32 (s / 4) + c) + s % 4 of the row, so that chain c's dwords of four consecutive steps form one 16-byte chunk and
+// a lane loads exactly its chain's operands, in step order.  H % 512 == 0.
+__host__ __device__ __forceinline__ size_t ck_chain_dword(int H, int e, int k) {
+    const int s = k >> 5, c = k & 31;
+    return (size_t)e * (H / 2) + 4 * (32 * (s >> 2) + c) + (s & 3);
+}
+
+// Two rows per wavefront from the chain-ordered table: lanes 0-31 run row `row0`'s 32 chains, lanes 32-63 row
+// `row1`'s (each a row base in u32x4 units), with the tokens read from shared memory as dwords (xd as in ck_row_dot).
+// The same order as ck_row_dot, without passing the weights through shared memory: chain c's 16-byte chunk q holds
+// its dwords of steps 4q .. 4q + 3.  Lanes 0 and 32 return their row's results.
+namespace ckdot {
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2f lds_v2f;
+
+// One token in fp32 (xf: element 2k + j of the token at xf[2k + j]): chunks q0 .. q0 + N - 1 of a lane's chain, the
+// element pairs of 8 chunks read together (one 8-byte read per step), no conversions of the token.
+template <int N>
+__device__ __forceinline__ void chain_consume_f32(const v4u* w, int q0, const lds_v2f* xfc, float& acc) {
+    constexpr int G = 8 < N ? 8 : N;
+    static_assert(N % G == 0, "chunk groups");
+#pragma unroll
+    for (int g = 0; g < N; g += G) {
+        v2f xv[G * 4];
+#pragma unroll
+        for (int u = 0; u < G; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[4 * u + i] = xfc[32 * (4 * (q0 + g + u) + i)];
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const unsigned wv = w[g + u][i];
+                acc = fmaf(hi(wv), xv[4 * u + i].y, acc);
+                acc = fmaf(lo(wv), xv[4 * u + i].x, acc);
+            }
+        }
+    }
+}
+
+// Chunks q0 .. q0 + N - 1 of a lane's chain (N a compile-time count, no branches): the token dwords of XG chunks
+// (4 XG steps x NT tokens, at most 32) are read from shared memory together, then consumed in step order.
+template <int NT, int N>
+__device__ __forceinline__ void chain_consume(const v4u* w, int q0, int T, int hd, const lds_u32* xc, float* acc) {
+    constexpr int XG = NT >= 8 ? 1 : NT >= 4 ? 2 : NT >= 2 ? 4 : 8;
+    constexpr int G = XG < N ? XG : N;
+    static_assert(N % G == 0, "chunk groups");
+#pragma unroll
+    for (int g = 0; g < N; g += G) {
+        unsigned xv[G * 4][NT];
+#pragma unroll
+        for (int u = 0; u < G; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) xv[4 * u + i][t] = xc[(t < T ? t : 0) * hd + 32 * (4 * (q0 + g + u) + i)];
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const unsigned wv = w[g + u][i];
+                const float w0 = lo(wv), w1 = hi(wv);
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[t] = fmaf(w1, hi(xv[4 * u + i][t]), acc[t]);
+                    acc[t] = fmaf(w0, lo(xv[4 * u + i][t]), acc[t]);
+                }
+            }
+        }
+    }
+}
+}  // namespace ckdot
+
+// H = 256 * QN (QN = 8 or 16): every load of the row issued at once, the rest without branches.  Other H (a multiple
+// of 512): two chunks per round trip.  xf (NT = 1 only, may be null): the token also staged in fp32, which saves the
+// token's conversions (the products and sums are the same).
+template <int NT, typename AfterIssue>
+__device__ __forceinline__ void ck_rows_dot_chain(const ckdot::v4u* __restrict__ row0, const ckdot::v4u* __restrict__ row1,
+                                                  int H, int T, const ckdot::lds_u32* xd, const ckdot::lds_f32* xf,
+                                                  float* acc, AfterIssue after_issue) {
+    using namespace ckdot;
+    const int lane = threadIdx.x & 63, c = lane & 31;
+    const int nq = H / 256, hd = H / 2;
+    const v4u* p = (lane < 32 ? row0 : row1) + c;
+    const lds_u32* xc = xd + c;
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.f;
+    auto fixed = [&](auto qn) __attribute__((always_inline)) {
+        constexpr int QN = decltype(qn)::value;
+        v4u w[QN];
+#pragma unroll
+        for (int q = 0; q < QN; q++) w[q] = __builtin_nontemporal_load(p + 32 * q);
+        after_issue();
+        if (NT == 1 && xf) chain_consume_f32<QN>(w, 0, (const lds_v2f*)xf + c, acc[0]);
+        else chain_consume<NT, QN>(w, 0, T, hd, xc, acc);
+    };
+    if (nq == 16) {
+        fixed(std::integral_constant<int, 16>());
+    } else if (nq == 8) {
+        fixed(std::integral_constant<int, 8>());
+    } else {
+        v4u w[2];
+#pragma unroll 1
+        for (int q0 = 0; q0 < nq; q0 += 2) {
+            w[0] = __builtin_nontemporal_load(p + 32 * q0);
+            w[1] = __builtin_nontemporal_load(p + 32 * (q0 + 1));
+            if (q0 == 0) after_issue();
+            chain_consume<NT, 2>(w, q0, T, hd, xc, acc);
         }
     }
 #pragma unroll

@@ -7,6 +7,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -59,7 +60,7 @@ struct moe_gpu {
     Sync* d_sync = nullptr;
     uint64_t* d_act = nullptr;      // tagged SiLU(g)*u pairs
     uint64_t* d_ypart = nullptr;    // tagged down outputs
-    uint16_t* d_stage = nullptr;  // 3*F*H bf16 staging for host loads
+    uint16_t* d_stage = nullptr;  // max(3F, E) * H bf16 staging for host loads (an expert, or the router table)
     int8_t* d_stage_q8 = nullptr;
     float* d_stage_sc = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -474,7 +475,7 @@ int moe_gpu_create(int device, int H, int F, int E, int topk, int n_shared, int 
     // split gate|up partials: at most max_tokens * (n_shared + topk) (slot, token) pairs, 4 parts per tile
     c->gpart_bytes = (size_t)max_tokens * kq * (F / 32) * moe::kMaxKp * 64 * 8;
     if ((rc = dev_alloc(c, (void**)&c->d_gpart, c->gpart_bytes, "gate|up partials"))) return bail(rc);
-    if ((rc = dev_alloc(c, (void**)&c->d_stage, (size_t)3 * F * H * 2, "staging"))) return bail(rc);
+    if ((rc = dev_alloc(c, (void**)&c->d_stage, (size_t)std::max(3 * F, E) * H * 2, "staging"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage_q8, (size_t)3 * F * H, "int8 staging"))) return bail(rc);
     if ((rc = dev_alloc(c, (void**)&c->d_stage_sc, (size_t)(2 * F + H) * 4, "scale staging"))) return bail(rc);
     if (hipMemset(c->d_slots, 0, sizeof(Slots)) != hipSuccess || hipMemset(c->d_sync, 0, sizeof(Sync)) != hipSuccess ||
@@ -573,7 +574,8 @@ int moe_gpu_load_router(moe_gpu* c, int layer, const uint16_t* wr, const float* 
     if (!wr) return fail(c, MOE_GPU_EINVAL, "NULL router weight");
     if ((rc = ensure_router(c, layer))) return rc;
     Layer& L = c->layers[layer];
-    HIPCHK(c, hipMemcpyAsync(L.wr, wr, (size_t)c->d.E * c->d.H * 2, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_stage, wr, (size_t)c->d.E * c->d.H * 2, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, moe::launch_relayout_router(c->d_stage, c->d.E, c->d.H, L.wr, c->stream));
     if (bias) HIPCHK(c, hipMemcpyAsync(L.bias, bias, (size_t)c->d.E * 4, hipMemcpyHostToDevice, c->stream));
     else HIPCHK(c, hipMemsetAsync(L.bias, 0, (size_t)c->d.E * 4, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -804,7 +806,9 @@ int moe_gpu_synth_layer(moe_gpu* c, int layer, uint64_t seed, float cw, const fl
     Layer& L = c->layers[layer];
     const Dims& d = c->d;
     auto tid = [&](int e, int m) { return ((uint64_t)layer * 4096 + (uint64_t)e) * 4 + (uint64_t)m; };
-    HIPCHK(c, moe::launch_synth_fill(L.wr, (uint64_t)d.E * d.H, moe::synth_key(seed, tid(4095, 0)), 0, cw, c->stream));
+    HIPCHK(c, moe::launch_synth_fill(c->d_stage, (uint64_t)d.E * d.H, moe::synth_key(seed, tid(4095, 0)), 0, cw,
+                                     c->stream));
+    HIPCHK(c, moe::launch_relayout_router(c->d_stage, d.E, d.H, L.wr, c->stream));
     if (bias) HIPCHK(c, hipMemcpyAsync(L.bias, bias, (size_t)d.E * 4, hipMemcpyHostToDevice, c->stream));
     else HIPCHK(c, hipMemsetAsync(L.bias, 0, (size_t)d.E * 4, c->stream));
     for (int e = 0; e < d.E; e++)

@@ -16,7 +16,10 @@ constexpr int kMaxTopk = 8;
 constexpr int kMaxShared = 4;
 constexpr int kMaxExperts = 512;
 constexpr int kMaxSlots = kMaxShared + kMaxTokens * kMaxTopk;
-constexpr int kRouterRows = 4;     // router rows per router unit: one per wavefront
+#ifndef MOE_ROUTER_ROWS
+#define MOE_ROUTER_ROWS 8
+#endif
+constexpr int kRouterRows = MOE_ROUTER_ROWS;  // router rows per router unit (2, 4 or 8): two per wavefront
 
 // Routing rules of the compute calls (the flag bits MOE_GPU_ROUTE_* of the C ABI select them).
 enum RouteRule { kRouteSoftmax = 0, kRouteSigmoid = 1 };
@@ -113,8 +116,8 @@ struct Sync {
 
 // Unit trace record (fused kernel, optional): start, inputs ready, end (100 MHz s_memrealtime ticks), workgroup,
 // aux, aux2.  Inputs ready: routed gate|up part: routing known; combining down unit: the other terms in; else 0.
-// aux: gate|up finishing part: sibling partials in; down unit: act rows staged; else 0.  aux2: down unit: weight
-// stream done; else 0.
+// aux: gate|up finishing part: sibling partials in; down unit: act rows staged; router unit: its operands in (weights
+// loaded, tokens staged); else 0.  aux2: down unit: weight stream done; router unit: dot products done; else 0.
 constexpr int kTraceFields = 6;
 
 struct FusedArgs {
@@ -162,6 +165,8 @@ hipError_t launch_down(const ExpertArgs& a, hipStream_t st);
 hipError_t launch_fused(const FusedArgs& f, int wg_per_cu, int grid, hipStream_t st, int* grid_out);
 
 hipError_t launch_relayout_gu(const uint16_t* g, const uint16_t* u, int H, int F, uint16_t* dst, hipStream_t st);
+// router table [E][H] bf16 (row-major, src) -> the chain order the router units read (dst, same size)
+hipError_t launch_relayout_router(const uint16_t* src, int E, int H, uint16_t* dst, hipStream_t st);
 hipError_t launch_relayout_dn(const uint16_t* d, int H, int F, uint16_t* dst, hipStream_t st);
 hipError_t launch_relayout_q8(const int8_t* q, const float* sc, int H, int F, int8_t* gu_dst, int8_t* dn_dst,
                               float* sc_dst, hipStream_t st);

@@ -291,11 +291,13 @@ __device__ __forceinline__ void reduce_waves(lds_float* red, const float* acc, i
 //   xs    [T][H/8] u32x4      all tokens' activations, staged once per workgroup
 //   as    [NT][F/8] u32x4     one slot's act rows (down units)
 //   red   [4][NT][64] float   cross-wave reduction
+//   xf    [H] float           T = 1 only: the token in fp32, for the router units' dot products
 // (the routing table is static __shared__ memory: RouteTab)
 struct Lds {
     lds_u32x4* xs;
     lds_u32x4* as;
     lds_float* red;
+    lds_float* xf;  // T = 1 only, else null
 };
 
 // `as` also serves as route_local's scratch
@@ -307,7 +309,7 @@ __host__ __device__ inline size_t as_bytes(int NT, int F, int E) {
 
 #if MOE_COMMON
 size_t lds_bytes(int T, int NT, int H, int F, int E) {
-    return (size_t)T * (H / 8) * 16 + as_bytes(NT, F, E) + (size_t)4 * NT * 64 * 4;
+    return (size_t)T * (H / 8) * 16 + as_bytes(NT, F, E) + (size_t)4 * NT * 64 * 4 + (T == 1 ? (size_t)H * 4 : 0);
 }
 #endif  // MOE_COMMON
 
@@ -319,6 +321,8 @@ __device__ inline Lds lds_carve(unsigned char* base_generic, int T, int NT, int 
     s.as = (lds_u32x4*)base;
     base += as_bytes(NT, F, E);
     s.red = (lds_float*)base;
+    base += (size_t)4 * NT * 64 * 4;
+    s.xf = T == 1 ? (lds_float*)base : nullptr;
     return s;
 }
 
@@ -333,7 +337,8 @@ __device__ __forceinline__ u32x4 pack_bf16x8(const float* v) {
     return r;
 }
 
-// Stage the T tokens' activations into s.xs (every thread returns after the closing barrier).
+// Stage the T tokens' activations into s.xs, and at T = 1 also into s.xf as fp32 (every thread returns after the
+// closing barrier).
 //   plain: a copy of in.x;
 //   block mode: r = bf16(resid + attn_o) (main.rs:122), then RMSNorm (host.rs:71-76): ms = sum(r^2) / H,
 //   rs = 1 / sqrt(ms + eps), h = bf16(bf16(r * rs) * w).  The squares are summed in a fixed order (per thread over
@@ -341,11 +346,26 @@ __device__ __forceinline__ u32x4 pack_bf16x8(const float* v) {
 //   the same bits.  Each thread handles 16-byte chunks c = tid + j * kThreads, two per pass (H = 4096: one pass, one
 //   round trip for resid, attn_o and the norm weight together), with few registers: the router unit stages while
 //   its weight loads are held in registers.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef LDS_AS f32x4 lds_f32x4;
+__device__ __forceinline__ void store_f32x8(lds_float* dst, const float* f) {
+    reinterpret_cast<lds_f32x4*>(dst)[0] = f32x4{f[0], f[1], f[2], f[3]};
+    reinterpret_cast<lds_f32x4*>(dst)[1] = f32x4{f[4], f[5], f[6], f[7]};
+}
+
 __device__ __forceinline__ void stage_in(const Lds& s, const StageSrc& in, int T, int H) {
     const int n = T * (H / 8);
     if (!in.resid) {
         const u32x4* src = reinterpret_cast<const u32x4*>(in.x);
-        for (int i = threadIdx.x; i < n; i += blockDim.x) s.xs[i] = src[i];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const u32x4 v = src[i];
+            s.xs[i] = v;
+            if (s.xf) {
+                float f[8];
+                unpack8(v, f);
+                store_f32x8(s.xf + 8 * i, f);
+            }
+        }
         __syncthreads();
         return;
     }
@@ -400,6 +420,7 @@ __device__ __forceinline__ void stage_in(const Lds& s, const StageSrc& in, int T
 #pragma unroll
             for (int i = 0; i < 8; i++) h[i] = round_bf(round_bf(fr[i] * rs) * fw[i]);
             s.xs[t * nc + c] = pack_bf16x8(h);
+            if (s.xf) store_f32x8(s.xf + 8 * c, h);
         }
     }
     __syncthreads();
@@ -417,23 +438,34 @@ __device__ __forceinline__ void combine_store(const ExpertArgs& a, size_t o, flo
 }
 
 // --------------------------------------------------------------------------------------------------------------------
-// Unit: router rows, in the reference's own order (ck_row_dot, ck_dot.h): the logits are bit-identical to ck_gemv's
-// (track2_opt/solar_engine/csrc/cpu_kern.c:9-19, :31-35).  Wave w computes row e0 + w for all T tokens; its 1 KiB
-// segment buffer is carved from s.as, unused while a router unit runs.
+// Unit: router rows, in the reference's own order (ck_rows_dot_chain, ck_dot.h): the logits are bit-identical to
+// ck_gemv's (track2_opt/solar_engine/csrc/cpu_kern.c:9-19, :31-35).  The table is in chain order (ck_chain_dword);
+// wave w < kRouterRows / 2 computes rows e0 + 2w (lanes 0-31) and e0 + 2w + 1 (lanes 32-63) for all T tokens.
 // stage: the activations (from src) are staged once the weight loads are in flight.  src travels by value: an
 // address of a kernel argument would make the compiler copy the arguments to scratch memory.
 template <int NT>
 __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
                                             uint64_t* __restrict__ logits, float* __restrict__ logits_out,
-                                            unsigned epoch, bool stage, const StageSrc src) {
+                                            unsigned epoch, bool stage, const StageSrc src, bool stamp,
+                                            uint64_t& t_in, uint64_t& t_dot) {
+    static_assert(kRouterRows == 2 || kRouterRows == 4 || kRouterRows == 8, "two router rows per wavefront");
     const int wave = wave_id(), lane = threadIdx.x & 63;
-    const int e = e0 + wave;
+    if (2 * wave >= kRouterRows) {  // a wavefront without rows only takes part in the staging
+        if (stage) stage_in(s, src, T, H);
+        return;
+    }
+    const int ea = e0 + 2 * wave, e = ea + (lane >> 5);
     float acc[NT];
-    ck_row_dot<NT>(reinterpret_cast<const u32x4*>(wr + (size_t)min(e, E - 1) * H), H, T, s.as + wave * 64,
-                   (const LDS_AS unsigned*)s.xs, acc, [&]() __attribute__((always_inline)) {
-                       if (stage) stage_in(s, src, T, H);
-                   });
-    if (lane == 0 && e < E) {
+    const u32x4* w = reinterpret_cast<const u32x4*>(wr);
+    const size_t rs = (size_t)H / 8;  // u32x4 per row
+    ck_rows_dot_chain<NT>(w + (size_t)min(ea, E - 1) * rs, w + (size_t)min(ea + 1, E - 1) * rs, H, T,
+                          (const LDS_AS unsigned*)s.xs, NT == 1 ? s.xf : nullptr, acc,
+                          [&]() __attribute__((always_inline)) {
+                              if (stage) stage_in(s, src, T, H);
+                              if (stamp) t_in = __builtin_amdgcn_s_memrealtime();
+                          });
+    if (stamp) t_dot = __builtin_amdgcn_s_memrealtime();
+    if ((lane & 31) == 0 && e < E) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (t < T) {
@@ -1078,11 +1110,12 @@ __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T,
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
     const int e0 = blockIdx.x * kRouterRows;
-    if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
-    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
-    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
-    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
-    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in);
+    uint64_t u0 = 0, u1 = 0;  // stamps (unused)
+    if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
+    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
+    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
+    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
+    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
 }
 
 __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
@@ -1228,9 +1261,11 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                 // grid is not all resident).  Compute every router row here (the same bits: rewriting a logit that
                 // its unit also writes is harmless), then wait for them without a limit.
                 ensure_staged();
+                uint64_t u0 = 0, u1 = 0;  // stamps (unused)
                 for (int r = 0; r < f.nR; r++)
-                    router_unit<NT>(s, a.L.wr, r * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, false, a.in);
-                __syncthreads();  // the router segments in s.as are route_local's scratch next
+                    router_unit<NT>(s, a.L.wr, r * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, false, a.in,
+                                    false, u0, u1);
+                __syncthreads();
                 route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
                             a.d.E, a.d.k, a.keep, S, f.do_topk, f.rule, -1);
             }
@@ -1262,7 +1297,8 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
-            router_unit<NT>(s, a.L.wr, ur.idx * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, stage, a.in);
+            router_unit<NT>(s, a.L.wr, ur.idx * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, stage, a.in,
+                            f.trace != nullptr, t_aux, t_aux2);
             if (stage && threadIdx.x == 0) s_staged = 1;
         } else if (ur.kind == 1) {
             ensure_routed();
@@ -1361,6 +1397,19 @@ __global__ void relayout_dn_kernel(const uint16_t* __restrict__ d, int H, int F,
     const size_t c = (q / 64) % nc;
     const int tile = (int)(q / (64 * nc));
     dst[q] = reinterpret_cast<const u32x4*>(d + (size_t)(tile * 64 + i) * F)[c];
+}
+
+// Router table [E][H] bf16 -> chain order (ck_chain_dword): one thread per destination 16-byte chunk.
+__global__ void relayout_router_kernel(const unsigned* __restrict__ src, int E, int H, u32x4* __restrict__ dst) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per_row = H / 8;
+    if (q >= (size_t)E * per_row) return;
+    const int e = (int)(q / per_row), r = (int)(q % per_row), qq = r / 32, c = r % 32;
+    const unsigned* row = src + (size_t)e * (H / 2);
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = row[32 * (4 * qq + i) + c];
+    dst[q] = v;
 }
 
 // q in ck_place_expert_q8 layout ([2F rows of H][H rows of F]) <-> tiled int8 + tile-ordered scales (dir 1 = back).
@@ -1636,6 +1685,13 @@ hipError_t launch_relayout_gu(const uint16_t* g, const uint16_t* u, int H, int F
     const size_t n = (size_t)(F / 32) * (H / 8) * 64;
     hipLaunchKernelGGL(relayout_gu_kernel, dim3(nblk(n, 256)), dim3(256), 0, st, g, u, H, F,
                        reinterpret_cast<u32x4*>(dst));
+    return hipGetLastError();
+}
+
+hipError_t launch_relayout_router(const uint16_t* src, int E, int H, uint16_t* dst, hipStream_t st) {
+    const size_t n = (size_t)E * (H / 8);
+    hipLaunchKernelGGL(relayout_router_kernel, dim3(nblk(n, 256)), dim3(256), 0, st,
+                       reinterpret_cast<const unsigned*>(src), E, H, reinterpret_cast<u32x4*>(dst));
     return hipGetLastError();
 }
 

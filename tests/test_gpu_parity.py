@@ -721,8 +721,9 @@ def test_solar_shared_ksplit_paths_and_bars(solar, kp, kps):
 
 
 def test_solar_unit_trace(solar):
-    """The fused kernel's unit trace: one record per unit of the work list, stamps in order within each unit (down
-    units: act staged, then stream done; the tile's combining unit: other terms in after its stream), and tracing
+    """The fused kernel's unit trace: one record per unit of the work list, stamps in order within each unit (router
+    units: operands in, then dot products done; down units: act staged, then stream done; the tile's combining unit:
+    other terms in after its stream), and tracing
     leaves the output bits unchanged."""
     from moe_gpu import OPT_LAST_GRID
     tier, hl = solar
@@ -737,13 +738,16 @@ def test_solar_unit_trace(solar):
     finally:
         tier.trace_units(False)
     np.testing.assert_array_equal(out.view(np.uint32), base.view(np.uint32))
-    nR, maxs, S, nht, ntile, kp = (SOLAR.E + 3) // 4, SOLAR.n_shared + SOLAR.k, SOLAR.n_shared, SOLAR.H // 64, \
+    nR, maxs, S, nht, ntile, kp = (SOLAR.E + 7) // 8, SOLAR.n_shared + SOLAR.k, SOLAR.n_shared, SOLAR.H // 64, \
         SOLAR.F // 32, 2
     assert tr.shape == (nR + 1 + maxs * ntile * kp + maxs * nht, 6)
     start, ready, end, wg, aux, aux2 = tr.T
     assert np.all(start > 0) and np.all(end >= start)
     assert np.all((wg >= 0) & (wg < grid))
-    down = aux2 > 0
+    router = np.arange(len(tr)) < nR
+    assert np.all(start[router] <= aux[router]) and np.all(aux[router] <= aux2[router])
+    assert np.all(aux2[router] <= end[router])
+    down = (aux2 > 0) & ~router
     assert down.sum() == maxs * nht
     assert np.all(start[down] <= aux[down]) and np.all(aux[down] <= aux2[down]) and np.all(aux2[down] <= end[down])
     comb = down & (ready > 0)
