@@ -150,10 +150,12 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
  * that their consumers poll); 0 runs
  * one kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in
  * workgroups per CU (default 1; 0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused
- * launch.  MOE_GPU_OPT_KSPLIT: K parts per routed gate|up tile, 1, 2 or 4 (0 = automatic: about 128 K weights per
- * part); it changes the summation order, identically in both paths.  MOE_GPU_OPT_KSPLIT_SHARED: the same for the shared
- * experts' tiles (0 = automatic, the same rule).  MOE_GPU_OPT_LAG: fused queue order, a routed slot's down
- * tiles are queued after the gate|up parts of the routed slot `lag` places later (0 = automatic).  MOE_GPU_OPT_SHARED_WAITS: 1
+ * launch.  MOE_GPU_OPT_KSPLIT: K parts per routed gate|up tile, 1, 2 or 4 (0 = automatic: whole tiles); it changes the
+ * summation order, identically in both paths.
+ * MOE_GPU_OPT_KSPLIT_SHARED: the same for the shared experts' tiles (0 = automatic: about 64 K weights per part, 128 K
+ * in MOE_GPU_INT8 calls).
+ * MOE_GPU_OPT_LAG: fused queue order, a routed slot's down tiles are queued after the gate|up parts of the routed
+ * slot `lag` places later (0 = automatic: 8).  MOE_GPU_OPT_SHARED_WAITS: 1
  * holds the shared experts' gate|up parts until the routing is known (0 = stream them while routing).
  * MOE_GPU_OPT_GRID: fused grid size in workgroups (0 = automatic: what fits at once); a larger grid is allowed (units
  * are handed out by a queue to running workgroups only, so a grid that is not all resident still completes).

@@ -131,18 +131,16 @@ void run_experts(Shim& s, int E, const Slot* slots, const float* w, const uint16
     }
 }
 
-// Slot of an expert given by (g, u, d) pointers.  reload = false: uploaded on first use only (the engine's mmap'd
-// safetensors weights are immutable and keep their addresses); reload = true (a placement call): uploaded now, into the
-// slot the key already has, if any (a host buffer can be freed and its address reused for another expert).
-bool slot_of_gud(Shim& s, const uint16_t* g, const uint16_t* u, const uint16_t* d, Slot* out, bool reload = false) {
+// Slot of an expert given by (g, u, d) pointers, uploaded on first use only (the engine's mmap'd safetensors weights
+// are immutable and keep their addresses).
+bool slot_of_gud(Shim& s, const uint16_t* g, const uint16_t* u, const uint16_t* d, Slot* out) {
     auto it = s.bf16.find(g);
-    if (it != s.bf16.end() && !reload) {
+    if (it != s.bf16.end()) {
         *out = it->second;
         return true;
     }
     Slot sl;
-    if (it != s.bf16.end()) sl = it->second;
-    else if (!new_slot(s, &sl)) return false;
+    if (!new_slot(s, &sl)) return false;
     if (!tier_ok(s, moe_gpu_load_expert(s.tier, sl.layer, sl.e, g, u, d), "moe_gpu_load_expert")) return false;
     s.bf16[g] = sl;
     *out = sl;
@@ -253,10 +251,15 @@ void ck_place_expert_q8(const uint16_t* g, const uint16_t* u, const uint16_t* d,
     Shim& s = shim();
     std::lock_guard<std::mutex> lock(s.mu);
     if (!ensure_tier(s, H, F)) return;
-    // quantise on the GPU (quant_row's rule, bit-identical): the bf16 expert goes to a slot, which keeps it (a later
-    // bf16 call on the same pointers reuses it), its int8 copy is read back into the caller's buffers
+    // quantise on the GPU (quant_row's rule, bit-identical): the bf16 expert goes to the slot of the caller's q
+    // buffer (placing into the same buffer again reuses it; any other buffer gets a slot of its own, so that freed and
+    // reused host addresses of g / u / d never make two placed experts share a slot), and its int8 copy is read back
+    // into the caller's buffers
     Slot sl;
-    if (!slot_of_gud(s, g, u, d, &sl, true)) return;
+    auto it = s.q8.find(qbuf);
+    if (it != s.q8.end()) sl = it->second;
+    else if (!new_slot(s, &sl)) return;
+    if (!tier_ok(s, moe_gpu_load_expert(s.tier, sl.layer, sl.e, g, u, d), "moe_gpu_load_expert")) return;
     if (!tier_ok(s, moe_gpu_quantize_experts(s.tier, sl.layer, sl.e, sl.e + 1), "moe_gpu_quantize_experts")) return;
     if (!tier_ok(s, moe_gpu_get_expert_q8(s.tier, sl.layer, sl.e, qbuf, sc), "moe_gpu_get_expert_q8")) return;
     const int rows = 2 * F + H;

@@ -315,19 +315,23 @@ int next_epoch(moe_gpu* c, unsigned* ep) {
     return MOE_GPU_OK;
 }
 
-// K parts per gate|up tile: the option, else about 128 K weights per part (64 rows x H / kp; 256 KiB of bf16, 128 KiB
-// of int8), the size that measured best for the fused schedule at H = 4096 in both precisions (smaller parts add
-// per-unit latency, larger ones a longer tail).
-static int kparts_auto(int H) {
+// K parts per gate|up tile: the option, else (Solar, H = 4096, measured on the fused schedule, us per call):
+//  - routed tiles whole (kp 1) at every batch: kp 2 -> 1 measured batch 1 59.6 -> 59.4, batch 2 92.6 -> 92.4,
+//    batch 4 147.4 -> 137.7, batch 8 268 -> 240, int8 38.6 -> 38.3; one rule for every batch also keeps a token's
+//    result independent of the batch it is in (the K split sets the summation order);
+//  - shared tiles (bf16 in every call): about 64 K weights per part in bf16 calls (kps 2 -> 4: 61.2 -> 60.2 at batch 1),
+//    so that the routing-independent work spreads over more workgroups while the routing is computed; 128 K in int8
+//    calls, whose routed work is smaller (kps 4 -> 2: 38.6 -> 37.3).
+static int kparts_auto(int H, size_t per_part) {
     const size_t weights = (size_t)64 * H;
     int kp = 1;
-    while (kp < moe::kMaxKp && weights / (kp * 2) >= ((size_t)128 << 10)) kp *= 2;
+    while (kp < moe::kMaxKp && weights / (kp * 2) >= per_part) kp *= 2;
     return kp;
 }
-static int kparts(const moe_gpu* c) { return c->ksplit > 0 ? c->ksplit : kparts_auto(c->d.H); }
-// The shared experts' parts (bf16 in every call) can be set apart from the routed experts'.
-static int kparts_shared(const moe_gpu* c) {
-    return c->ksplit_shared > 0 ? c->ksplit_shared : kparts_auto(c->d.H);
+static int kparts(const moe_gpu* c) { return c->ksplit > 0 ? c->ksplit : 1; }
+static int kparts_shared(const moe_gpu* c, bool int8) {
+    if (c->ksplit_shared > 0) return c->ksplit_shared;
+    return kparts_auto(c->d.H, (size_t)(int8 ? 128 : 64) << 10);
 }
 
 // The expert pipeline of one call.  do_topk: route on the device from the layer's router (ids/gates are outputs);
@@ -351,7 +355,7 @@ int run_layer(moe_gpu* c, int layer, int T, const moe::StageSrc& in, int32_t* id
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
     a.kp = kparts(c);
-    a.kps = kparts_shared(c);
+    a.kps = kparts_shared(c, a.int8 != 0);
     a.gpart = c->d_gpart;
     if ((rc = next_epoch(c, &a.epoch))) return rc;
     a.err = &c->d_sync->err;

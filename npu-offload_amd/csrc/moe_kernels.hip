@@ -790,7 +790,7 @@ __device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int
 // the slot's tokens.  Sums: wavefronts in order within a part, then parts in order.  Parts below kp - 1 publish their
 // partial sums to gpart; part kp - 1 (the tile's last unit in queue order) reads them back, finishes the tile and
 // publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
-template <int N>
+template <int N, bool Q8OK>
 __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
                                             const int* tok, int pair0, uint64_t& stamp) {
     const int H = a.d.H, F = a.d.F, kp = e < 0 ? a.kps : a.kp, ntile = F / 32;
@@ -802,7 +802,7 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
     float acc[N];
 #pragma unroll
     for (int j = 0; j < N; j++) acc[j] = 0.f;
-    const bool q8 = a.int8 && e >= 0;
+    const bool q8 = Q8OK && a.int8 && e >= 0;  // Q8OK false: no int8 code in this instantiation
     if (!q8) {
         const uint16_t* base =
             e >= 0 ? a.L.gu + (size_t)e * a.d.gu_stride() : a.L.sgu + (size_t)(-1 - e) * a.d.gu_stride();
@@ -858,14 +858,14 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
     __syncthreads();  // s.red is reused by the next unit
 }
 
-template <int NT>
+template <int NT, bool Q8OK = true>
 __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
                                             const int* tok, int pair0, uint64_t& stamp) {
-    if (ntok <= 1 || NT == 1) gateup_core<1>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else gateup_core<NT>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    if (ntok <= 1 || NT == 1) gateup_core<1, Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else gateup_core<NT, Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
 }
 
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
@@ -885,7 +885,7 @@ __device__ __forceinline__ bool combine_in_unit(const ExpertArgs& a) {
     return a.T * 64 * (a.d.n_shared + a.d.k) <= kCombW * kThreads;
 }
 
-template <int N>
+template <int N, bool Q8OK>
 __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank, DownStamps& st, bool comb, const lds_RouteTab* crt) {
     const int H = a.d.H, F = a.d.F;
@@ -893,7 +893,7 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     const int nc = F / 8;
     // the weight stream starts first: its first bank is in flight while the act rows are polled (a second bank
     // here, or the act loads ahead of the bank, measured slower)
-    const bool q8 = a.int8 && e >= 0;
+    const bool q8 = Q8OK && a.int8 && e >= 0;  // Q8OK false: no int8 code in this instantiation
     TileStream<N, false, MOE_DN_DEPTH> tb;
     TileStream<N, true, MOE_DN_DEPTH> tq;
     if (!q8) {
@@ -1017,14 +1017,14 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     __syncthreads();  // s.as / s.red are reused by the next unit
 }
 
-template <int NT>
+template <int NT, bool Q8OK = true>
 __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank, DownStamps& st, bool comb = false, const lds_RouteTab* crt = nullptr) {
-    if (ntok <= 1 || NT == 1) down_core<1>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else down_core<NT>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    if (ntok <= 1 || NT == 1) down_core<1, Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else down_core<NT, Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
 }
 
 // Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
@@ -1225,7 +1225,7 @@ __device__ __forceinline__ UnitRef decode_unit(int u, int uR, int S, int M, int 
     return {3, S + n1 + u / nht, u % nht};  // downs of the last routed slots
 }
 
-template <int NT>
+template <int NT, bool Q8OK>
 __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ RouteTab rt_mem;
@@ -1313,7 +1313,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                     int tok[NT];
 #pragma unroll
                     for (int j = 0; j < NT; j++) tok[j] = j;
-                    gateup_unit<NT>(s, a, sl, tile, kpi, -1 - sl, a.T, tok, sl * a.T, aux);
+                    gateup_unit<NT, Q8OK>(s, a, sl, tile, kpi, -1 - sl, a.T, tok, sl * a.T, aux);
                 }
             } else {
                 ensure_routed();
@@ -1321,7 +1321,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                 if (sl < rt->nslot) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
-                    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, aux);
+                    gateup_unit<NT, Q8OK>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, aux);
                 }
             }
         } else {
@@ -1337,7 +1337,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                         tok[j] = j;
                         rank[j] = -1;
                     }
-                    down_unit<NT>(s, a, sl, ht, -1 - sl, a.T, tok, rank, ds);
+                    down_unit<NT, Q8OK>(s, a, sl, ht, -1 - sl, a.T, tok, rank, ds);
                 }
             } else {
                 ensure_routed();
@@ -1345,7 +1345,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
                     SlotRt<NT> v;
                     v.load(rt, sl, S, a.keep);
                     const bool fold = sl == maxs - 1 && combine_in_unit(a);
-                    down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, ds, fold, rt);
+                    down_unit<NT, Q8OK>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, ds, fold, rt);
                     combined = fold;
                 }
             }
@@ -1640,20 +1640,24 @@ hipError_t launch_down(const ExpertArgs& ea, hipStream_t st) {
 
 template <int NT>
 hipError_t fused_nt(FusedArgs f, int wg_per_cu, int grid_req, hipStream_t st, int* grid_out) {
-    const void* fn = reinterpret_cast<const void*>(&fused_layer_kernel<NT>);
+    // int8 routed experts get their own instantiation: the bf16 kernel carries no int8 code
+    auto kern = f.e.int8 ? &fused_layer_kernel<NT, true> : &fused_layer_kernel<NT, false>;
+    const void* fn = reinterpret_cast<const void*>(kern);
     const size_t lds = lds_bytes(f.e.T, NT, f.e.d.H, f.e.d.F, f.e.d.E);
     // occupancy per (device, LDS size), computed once: the launch itself stays a single host call
     static thread_local int c_dev = -1, c_ncu = 0, c_per_cu = 0;
     static thread_local size_t c_lds = 0;
+    static thread_local const void* c_fn = nullptr;
     hipError_t e;
     int dev = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
     if ((e = set_lds(fn, lds)) != hipSuccess) return e;
-    if (dev != c_dev || lds != c_lds) {
+    if (dev != c_dev || lds != c_lds || fn != c_fn) {
         if ((e = hipDeviceGetAttribute(&c_ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
         if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&c_per_cu, fn, 256, lds)) != hipSuccess) return e;
         c_dev = dev;
         c_lds = lds;
+        c_fn = fn;
     }
     int per_cu = c_per_cu, ncu = c_ncu;
     if (wg_per_cu > 0 && wg_per_cu < per_cu) per_cu = wg_per_cu;
@@ -1662,7 +1666,7 @@ hipError_t fused_nt(FusedArgs f, int wg_per_cu, int grid_req, hipStream_t st, in
     int grid = grid_req > 0 ? grid_req : ncu * per_cu;  // a requested grid may exceed what fits at once
     if (grid > units) grid = units;
     if (grid_out) *grid_out = grid;
-    hipLaunchKernelGGL(fused_layer_kernel<NT>, dim3(grid), dim3(256), lds, st, f);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, f);
     return hipGetLastError();
 }
 

@@ -114,8 +114,11 @@ def test_shim_int8_matches_cpu_kern():
     rng = np.random.default_rng(62)
     H, F, n = 1024, 512, 4
     qs, scs = [], []
+    g, u, d = np.empty((F, H), np.uint16), np.empty((F, H), np.uint16), np.empty((H, F), np.uint16)
     for _ in range(n):
-        g, u, d = bf(rng, (F, H), 0.02), bf(rng, (F, H), 0.02), bf(rng, (H, F), 0.02)
+        # the same g / u / d buffers for every expert, refilled in place: each placed expert must still get its own
+        # slot (placements are keyed by the caller's q buffer, not by the source addresses)
+        g[:], u[:], d[:] = bf(rng, (F, H), 0.02), bf(rng, (F, H), 0.02), bf(rng, (H, F), 0.02)
         q = np.zeros(3 * F * H, np.int8); sc = np.zeros(2 * F + H, np.float32); rs = np.zeros(2 * F + H, np.int32)
         L.ck_place_expert_q8(g.ctypes.data, u.ctypes.data, d.ctypes.data, q.ctypes.data, sc.ctypes.data, rs.ctypes.data,
                               H, F)

@@ -738,9 +738,9 @@ def test_solar_unit_trace(solar):
     finally:
         tier.trace_units(False)
     np.testing.assert_array_equal(out.view(np.uint32), base.view(np.uint32))
-    nR, maxs, S, nht, ntile, kp = (SOLAR.E + 7) // 8, SOLAR.n_shared + SOLAR.k, SOLAR.n_shared, SOLAR.H // 64, \
-        SOLAR.F // 32, 2
-    assert tr.shape == (nR + 1 + maxs * ntile * kp + maxs * nht, 6)
+    nR, maxs, S, nht, ntile = (SOLAR.E + 7) // 8, SOLAR.n_shared + SOLAR.k, SOLAR.n_shared, SOLAR.H // 64, SOLAR.F // 32
+    kp, kps = 1, 4  # automatic K parts at H = 4096 in a bf16 call: routed, shared
+    assert tr.shape == (nR + 1 + S * ntile * kps + (maxs - S) * ntile * kp + maxs * nht, 6)
     start, ready, end, wg, aux, aux2 = tr.T
     assert np.all(start > 0) and np.all(end >= start)
     assert np.all((wg >= 0) & (wg < grid))
