@@ -145,13 +145,14 @@ uint64_t moe_gpu_synth_key(uint64_t seed, uint64_t tensor_id);
 /* Duration in ms of the last compute call's kernels when timing is enabled (hipEvents on the context stream). */
 int moe_gpu_enable_timing(moe_gpu* ctx, int on);
 int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
-/* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call is one persistent kernel that walks router
+/* Execution options.  MOE_GPU_OPT_FUSED (default 1): each layer/moe call of up to 8 tokens (calls of 9 to 16 tokens,
+ * possible for H <= 3072, always take the unfused kernels) is one persistent kernel that walks router
  * rows, top-k/grouping, gate|up tile parts and down tiles (a work queue; cross-workgroup values are epoch-tagged words
  * that their consumers poll); 0 runs
  * one kernel per phase (same arithmetic, bit-identical results).  MOE_GPU_OPT_WG_PER_CU: fused grid size in
  * workgroups per CU (default 1; 0 = as many as fit).  MOE_GPU_OPT_LAST_GRID (read only): grid of the last fused
- * launch.  MOE_GPU_OPT_KSPLIT: K parts per routed gate|up tile, 1, 2 or 4 (0 = automatic: whole tiles); it changes the
- * summation order, identically in both paths.
+ * launch.  MOE_GPU_OPT_KSPLIT: K parts per routed gate|up tile, 1, 2 or 4 (0 = automatic: whole tiles in bf16 calls,
+ * about 128 K weights per part in MOE_GPU_INT8 calls); it changes the summation order, identically in both paths.
  * MOE_GPU_OPT_KSPLIT_SHARED: the same for the shared experts' tiles (0 = automatic: about 64 K weights per part, 128 K
  * in MOE_GPU_INT8 calls).
  * MOE_GPU_OPT_LAG: fused queue order, a routed slot's down tiles are queued after the gate|up parts of the routed
@@ -177,6 +178,8 @@ int moe_gpu_last_time_ms(moe_gpu* ctx, float* ms);
 #define MOE_GPU_ROUTE_SIGMOID 1
 int moe_gpu_set_option(moe_gpu* ctx, int opt, int value);
 int moe_gpu_get_option(moe_gpu* ctx, int opt, int* value);
+/* The context's shape as created (any pointer may be NULL). */
+int moe_gpu_get_shape(moe_gpu* ctx, int* H, int* F, int* E, int* topk, int* n_shared, int* n_layers);
 /* Unit trace of the fused kernel: with on != 0, each fused launch records for every unit of its work list
  * {start, inputs ready, end, workgroup, aux, aux2} in the 100 MHz s_memrealtime clock.  Inputs ready: a routed gate|up
  * part's routing known, a combining down unit's other terms in, else 0; aux: a gate|up tile's finishing part has its
@@ -304,6 +307,7 @@ int moe_model_synchronize(moe_model* m);
 int moe_model_load_layer(moe_model* m, int layer, const uint16_t* in_norm, const uint16_t* wq, const uint16_t* wk,
                          const uint16_t* wv, const uint16_t* wo, const uint16_t* post_norm);
 int moe_model_load_embedding(moe_model* m, const uint16_t* emb);                   /* [vocab, H] bf16 */
+int moe_model_get_config(moe_model* m, moe_model_config* cfg);                     /* the configuration as created */
 int moe_model_load_rope(moe_model* m, const uint16_t* cos_tab, const uint16_t* sin_tab); /* [max_ctx, D] bf16 */
 /* Steps run the first n layers (default all), then the head: a stage of a model split over several devices, or a
  * layer-by-layer check. */
@@ -317,6 +321,43 @@ int moe_model_step_dev(moe_model* m, const int32_t* token, int pos, int32_t* nex
 int moe_model_step(moe_model* m, int token, int pos, int32_t* next, float* best);
 /* The residual stream after the last layer of the last step (before the final norm), [H] bf16 to host or device. */
 int moe_model_residual(moe_model* m, uint16_t* x);
+
+/* ----------------------------------------------------------------------------------------------- weights on disk
+ * The model directory of safetensors files, replacing the engine's Weights (track2_opt/solar_engine/src/host.rs:78-117):
+ * every *.safetensors file of `dir`, in name order, memory-mapped read-only; tensors found by their HF names (a name in
+ * a later file replaces an earlier one).  The mapping stays until moe_st_close; pointers from moe_st_tensor are into
+ * it.  Headers are validated (offsets inside the file and matching dtype x shape), so a malformed file is an error,
+ * never a read outside the mapping. */
+typedef struct moe_st moe_st;
+#define MOE_ST_BF16 0
+#define MOE_ST_F32 1
+#define MOE_ST_F16 2
+#define MOE_ST_I8 3
+#define MOE_ST_I32 4
+#define MOE_ST_I64 5
+#define MOE_ST_U8 6
+int moe_st_open(const char* dir, moe_st** out);
+void moe_st_close(moe_st* st);
+const char* moe_st_last_error(const moe_st* st); /* st == NULL: the last failed open or placement read */
+int moe_st_count(const moe_st* st);              /* number of tensors */
+/* Tensor by name: data pointer into the mapping, byte size, MOE_ST_* dtype, shape; *ndim is the capacity of `shape` on
+ * entry, the tensor's rank on return.  Any output may be NULL.  MOE_GPU_EINVAL when absent. */
+int moe_st_tensor(const moe_st* st, const char* name, const void** data, size_t* nbytes, int* dtype, int64_t* shape,
+                  int* ndim);
+/* MoE half of model layer `model_layer` into the context's layer `tier_layer` (the engine's names: main.rs:466-468,
+ * :519; host.rs:111-116): router mlp.gate.weight [E, H] and mlp.gate.e_score_correction_bias [E] (fp32 or bf16; zero
+ * when absent), shared experts mlp.shared_experts.{gate,up,down}_proj.weight (n_shared > 1: mlp.shared_experts.{s}.*),
+ * and routed experts mlp.experts.{e}.{gate,up,down}_proj.weight for e in experts[0..n) (n < 0: every e < E).  Shapes
+ * are checked against the context. */
+int moe_st_load_moe_layer(const moe_st* st, moe_gpu* ctx, int model_layer, int tier_layer, const int32_t* experts,
+                          int n);
+/* A whole decode model: per layer the attention block (input_layernorm, self_attn.{q,k,v,o}_proj,
+ * post_attention_layernorm) and the MoE half (every expert), then model.embed_tokens.weight, lm_head.weight and
+ * model.norm.weight.  Shapes are checked against the model's configuration. */
+int moe_st_load_model(const moe_st* st, moe_model* m);
+/* The engine's placement.json (main.rs:455; moe_offload/placement.py:3): [layer][tier] -> expert ids in slot order.
+ * *n receives the count of (layer, tier)'s ids, written to ids when it fits `cap` (ids may be NULL to ask the count). */
+int moe_placement_read(const char* path, int layer, int tier, int32_t* ids, int cap, int* n);
 
 #ifdef __cplusplus
 }

@@ -41,7 +41,8 @@ def _jobs():
             (os.path.join(CSRC, "lm_head.hip"), [], os.path.join(obj, "lm_head.o")),
             (os.path.join(CSRC, "attn_decode.hip"), [], os.path.join(obj, "attn_decode.o")),
             (os.path.join(CSRC, "dense_ops.hip"), [], os.path.join(obj, "dense_ops.o")),
-            (os.path.join(CSRC, "decode_model.hip"), [], os.path.join(obj, "decode_model.o"))]
+            (os.path.join(CSRC, "decode_model.hip"), [], os.path.join(obj, "decode_model.o")),
+            (os.path.join(CSRC, "st_loader.cpp"), [], os.path.join(obj, "st_loader.o"))]
     for part in KERNEL_PARTS:
         jobs.append((os.path.join(CSRC, "moe_kernels.hip"), [f"-DMOE_PART={part}"],
                      os.path.join(obj, f"moe_kernels_part{part}.o")))

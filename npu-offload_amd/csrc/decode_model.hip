@@ -296,6 +296,14 @@ int moe_model_load_layer(moe_model* m, int layer, const uint16_t* in_norm, const
     return MOE_GPU_OK;
 }
 
+int moe_model_get_config(moe_model* m, moe_model_config* cfg) {
+    int rc = enter(m);
+    if (rc) return rc;
+    if (!cfg) return mfail(m, MOE_GPU_EINVAL, "NULL config");
+    *cfg = m->c;
+    return MOE_GPU_OK;
+}
+
 int moe_model_load_embedding(moe_model* m, const uint16_t* emb) {
     int rc = enter(m);
     if (rc) return rc;

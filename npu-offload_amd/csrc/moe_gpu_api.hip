@@ -316,9 +316,10 @@ int next_epoch(moe_gpu* c, unsigned* ep) {
 }
 
 // K parts per gate|up tile: the option, else (Solar, H = 4096, measured on the fused schedule, us per call):
-//  - routed tiles whole (kp 1) at every batch: kp 2 -> 1 measured batch 1 59.6 -> 59.4, batch 2 92.6 -> 92.4,
-//    batch 4 147.4 -> 137.7, batch 8 268 -> 240, int8 38.6 -> 38.3; one rule for every batch also keeps a token's
-//    result independent of the batch it is in (the K split sets the summation order);
+//  - routed tiles: whole (kp 1) in bf16 calls at every batch: kp 2 -> 1 measured batch 1 59.6 -> 59.4, batch 2
+//    92.6 -> 92.4, batch 4 147.4 -> 137.7, batch 8 268 -> 240; in int8 calls about 128 K weights per part (kp 2 at
+//    H = 4096: 39.0 -> 37.0 at batch 1 against whole tiles).  The rule depends on the precision only, so a token's
+//    result does not depend on the batch it is in (the K split sets the summation order);
 //  - shared tiles (bf16 in every call): about 64 K weights per part in bf16 calls (kps 2 -> 4: 61.2 -> 60.2 at batch 1),
 //    so that the routing-independent work spreads over more workgroups while the routing is computed; 128 K in int8
 //    calls, whose routed work is smaller (kps 4 -> 2: 38.6 -> 37.3).
@@ -328,7 +329,10 @@ static int kparts_auto(int H, size_t per_part) {
     while (kp < moe::kMaxKp && weights / (kp * 2) >= per_part) kp *= 2;
     return kp;
 }
-static int kparts(const moe_gpu* c) { return c->ksplit > 0 ? c->ksplit : 1; }
+static int kparts(const moe_gpu* c, bool int8) {
+    if (c->ksplit > 0) return c->ksplit;
+    return int8 ? kparts_auto(c->d.H, (size_t)128 << 10) : 1;
+}
 static int kparts_shared(const moe_gpu* c, bool int8) {
     if (c->ksplit_shared > 0) return c->ksplit_shared;
     return kparts_auto(c->d.H, (size_t)(int8 ? 128 : 64) << 10);
@@ -354,12 +358,12 @@ int run_layer(moe_gpu* c, int layer, int T, const moe::StageSrc& in, int32_t* id
     a.in = in; a.out = out; a.x_next = x_next; a.ids = ids; a.gates = gates;
     a.slots = c->d_slots; a.act = c->d_act; a.ypart = c->d_ypart;
     a.maxs = c->d.n_shared + T * keep;
-    a.kp = kparts(c);
+    a.kp = kparts(c, a.int8 != 0);
     a.kps = kparts_shared(c, a.int8 != 0);
     a.gpart = c->d_gpart;
     if ((rc = next_epoch(c, &a.epoch))) return rc;
     a.err = &c->d_sync->err;
-    if (c->fused) {
+    if (c->fused && T <= 8) {  // 9 to 16 tokens run the unfused kernels (the same arithmetic)
         FusedArgs f;
         f.e = a;
         f.logits = c->d_logits_tag;
@@ -911,6 +915,18 @@ int moe_gpu_read_trace(moe_gpu* c, uint64_t* buf, int max_units, int* units) {
     HIPCHK(c, hipStreamSynchronize(c->stream));
     HIPCHK(c, hipMemcpy(buf, c->d_trace, (size_t)n * moe::kTraceFields * sizeof(uint64_t), hipMemcpyDeviceToHost));
     *units = n;
+    return MOE_GPU_OK;
+}
+
+int moe_gpu_get_shape(moe_gpu* c, int* H, int* F, int* E, int* topk, int* n_shared, int* n_layers) {
+    int rc = enter(c);
+    if (rc) return rc;
+    if (H) *H = c->d.H;
+    if (F) *F = c->d.F;
+    if (E) *E = c->d.E;
+    if (topk) *topk = c->d.k;
+    if (n_shared) *n_shared = c->d.n_shared;
+    if (n_layers) *n_layers = c->n_layers;
     return MOE_GPU_OK;
 }
 

@@ -45,6 +45,9 @@ SYMBOLS = (
     "moe_model_create", "moe_model_destroy", "moe_model_last_error", "moe_model_experts", "moe_model_head",
     "moe_model_set_stream", "moe_model_synchronize", "moe_model_load_layer", "moe_model_load_embedding",
     "moe_model_load_rope", "moe_model_set_layers", "moe_model_kv_cache", "moe_model_step_dev", "moe_model_step", "moe_model_residual",
+    "moe_model_get_config", "moe_gpu_get_shape",
+    "moe_st_open", "moe_st_close", "moe_st_last_error", "moe_st_count", "moe_st_tensor", "moe_st_load_moe_layer",
+    "moe_st_load_model", "moe_placement_read",
 )
 ARGMAX_FP32, ARGMAX_BF16 = 0, 1
 OPT_FUSED, OPT_WG_PER_CU, OPT_LAST_GRID, OPT_KSPLIT, OPT_LAG, OPT_SHARED_WAITS, OPT_KSPLIT_SHARED = 1, 2, 3, 4, 5, 6, 7
@@ -163,6 +166,17 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_model_step_dev": (i, [vp, vp, i, vp, vp]),
         "moe_model_step": (i, [vp, i, i, C.POINTER(C.c_int32), C.POINTER(f)]),
         "moe_model_residual": (i, [vp, vp]),
+        "moe_model_get_config": (i, [vp, vp]),
+        "moe_gpu_get_shape": (i, [vp, vp, vp, vp, vp, vp, vp]),
+        "moe_st_open": (i, [C.c_char_p, C.POINTER(vp)]),
+        "moe_st_close": (None, [vp]),
+        "moe_st_last_error": (C.c_char_p, [vp]),
+        "moe_st_count": (i, [vp]),
+        "moe_st_tensor": (i, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(C.c_size_t), C.POINTER(i),
+                              C.POINTER(C.c_int64), C.POINTER(i)]),
+        "moe_st_load_moe_layer": (i, [vp, vp, i, i, vp, i]),
+        "moe_st_load_model": (i, [vp, vp]),
+        "moe_placement_read": (i, [C.c_char_p, i, i, vp, i, C.POINTER(i)]),
     }
     for name in SYMBOLS:
         fn = getattr(L, name)
@@ -603,6 +617,67 @@ class MoeModel:
         x = np.zeros(self.cfg.H, np.uint16)
         self._chk(self.L.moe_model_residual(self.h, _p(x)))
         return x
+
+
+ST_BF16, ST_F32, ST_F16, ST_I8, ST_I32, ST_I64, ST_U8 = 0, 1, 2, 3, 4, 5, 6
+
+
+class SafeTensors:
+    """A model directory of safetensors files, memory-mapped by the library (moe_st_*, the engine's Weights,
+    track2_opt/solar_engine/src/host.rs:78-117): tensors by HF name, and loads into a tier or a decode model."""
+
+    def __init__(self, directory: str):
+        self.L = load_library()
+        h = C.c_void_p()
+        rc = self.L.moe_st_open(directory.encode(), C.byref(h))
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_st_last_error(None).decode())
+        self.h = h
+
+    def _chk(self, rc: int):
+        if rc != OK:
+            raise MoeGpuError(rc, self.L.moe_st_last_error(self.h).decode())
+
+    def __len__(self) -> int:
+        return self.L.moe_st_count(self.h)
+
+    def tensor(self, name: str):
+        """(dtype code, shape, bytes) of a tensor (the bytes copied out of the mapping)."""
+        data, nb, dt = C.c_void_p(), C.c_size_t(), C.c_int()
+        shape = (C.c_int64 * 8)(); nd = C.c_int(8)
+        self._chk(self.L.moe_st_tensor(self.h, name.encode(), C.byref(data), C.byref(nb), C.byref(dt), shape,
+                                       C.byref(nd)))
+        return dt.value, tuple(shape[:nd.value]), C.string_at(data, nb.value)
+
+    def load_moe_layer(self, tier: "MoeGpu", model_layer: int, tier_layer: int, experts=None):
+        ids = None if experts is None else np.ascontiguousarray(experts, np.int32)
+        self._chk(self.L.moe_st_load_moe_layer(self.h, tier.h, model_layer, tier_layer, _p(ids),
+                                                -1 if ids is None else len(ids)))
+
+    def load_model(self, m: "MoeModel"):
+        self._chk(self.L.moe_st_load_model(self.h, m.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.moe_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+def placement_read(path: str, layer: int, tier: int) -> np.ndarray:
+    """Expert ids of (layer, tier) from the engine's placement.json (main.rs:455; moe_offload/placement.py:3)."""
+    L = load_library()
+    n = C.c_int()
+    rc = L.moe_placement_read(path.encode(), layer, tier, None, 0, C.byref(n))
+    if rc != OK:
+        raise MoeGpuError(rc, L.moe_st_last_error(None).decode())
+    ids = np.zeros(n.value, np.int32)
+    rc = L.moe_placement_read(path.encode(), layer, tier, _p(ids), n.value, C.byref(n))
+    if rc != OK:
+        raise MoeGpuError(rc, L.moe_st_last_error(None).decode())
+    return ids
 
 
 def gpu_moe(tier: MoeGpu, layer: int, x, experts: Sequence[int], toks: Sequence, ws: Sequence) -> np.ndarray:
