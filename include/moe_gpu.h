@@ -96,9 +96,10 @@ int moe_gpu_get_expert_q8(moe_gpu* ctx, int layer, int e, int8_t* q, float* sc);
 /* ----------------------------------------------------------------------------------------------- compute (host buffers)
  * Synchronous; x [T,H] bf16, out [T,H] fp32, ids/gates [T,k].  */
 
-/* Router GEMV + softmax top-k on the device: replaces ck_gemv(mlp.gate.weight) (cpu_kern.c:31-35, main.rs:129) or the
- * NPU shared_router logits (dense/shared.rs:191-210) followed by the host route() (host.rs:119-128).  keep <= 0 means
- * keep = k.  logits [T,E] may be NULL. */
+/* Router GEMV + top-k on the device (the context's routing rule, MOE_GPU_OPT_ROUTE_RULE: softmax by default, or
+ * Solar's sigmoid rule): replaces ck_gemv(mlp.gate.weight) (cpu_kern.c:31-35, main.rs:129; the logits are its bits) or
+ * the NPU shared_router logits (dense/shared.rs:191-210) followed by the host route() (host.rs:119-128).  keep <= 0
+ * means keep = k.  logits [T,E] may be NULL. */
 int moe_gpu_route(moe_gpu* ctx, int layer, int T, const uint16_t* x, int keep, int32_t* ids, float* gates,
                   float* logits);
 /* Grouped routed experts + shared experts + combine for caller-chosen ids/gates [T,k]: replaces ck_moe3

@@ -22,6 +22,10 @@ pub mod ffi {
         _private: [u8; 0],
     }
     #[repr(C)]
+    pub struct MoeSt {
+        _private: [u8; 0],
+    }
+    #[repr(C)]
     #[derive(Clone, Copy, Debug)]
     pub struct MoeModelConfig {
         pub h: c_int,
@@ -83,6 +87,14 @@ pub mod ffi {
         pub fn moe_model_load_embedding(m: *mut MoeModel, emb: *const u16) -> c_int;
         pub fn moe_model_load_rope(m: *mut MoeModel, cos_tab: *const u16, sin_tab: *const u16) -> c_int;
         pub fn moe_model_step(m: *mut MoeModel, token: c_int, pos: c_int, next: *mut i32, best: *mut f32) -> c_int;
+        pub fn moe_st_open(dir: *const c_char, out: *mut *mut MoeSt) -> c_int;
+        pub fn moe_st_close(st: *mut MoeSt);
+        pub fn moe_st_last_error(st: *const MoeSt) -> *const c_char;
+        pub fn moe_st_load_moe_layer(st: *const MoeSt, ctx: *mut MoeGpu, model_layer: c_int, tier_layer: c_int,
+                                     experts: *const i32, n: c_int) -> c_int;
+        pub fn moe_st_load_model(st: *const MoeSt, m: *mut MoeModel) -> c_int;
+        pub fn moe_placement_read(path: *const c_char, layer: c_int, tier: c_int, ids: *mut i32, cap: c_int,
+                                  n: *mut c_int) -> c_int;
     }
 }
 
@@ -243,4 +255,48 @@ impl Drop for GpuModel {
     fn drop(&mut self) {
         unsafe { ffi::moe_model_destroy(self.m) }
     }
+}
+
+/// The model directory's safetensors files, memory-mapped (Weights::open, host.rs:82-99), for loading a tier layer or
+/// a whole GpuModel by the engine's tensor names.
+pub struct Weights {
+    st: *mut ffi::MoeSt,
+}
+
+impl Weights {
+    pub fn open(dir: &str) -> Result<Self, Error> {
+        let c = std::ffi::CString::new(dir).map_err(|_| Error { code: -1, msg: "NUL in path".into() })?;
+        let mut st = std::ptr::null_mut();
+        let rc = unsafe { ffi::moe_st_open(c.as_ptr(), &mut st) };
+        check(rc, || cstr(unsafe { ffi::moe_st_last_error(std::ptr::null()) }))?;
+        Ok(Self { st })
+    }
+    fn ok(&self, rc: c_int) -> Result<(), Error> {
+        check(rc, || cstr(unsafe { ffi::moe_st_last_error(self.st) }))
+    }
+    /// Router, bias, shared experts and the listed routed experts (None: all) of model layer `l` into tier layer `tl`.
+    pub fn load_moe_layer(&self, tier: &mut GpuTier, l: usize, tl: usize, experts: Option<&[i32]>) -> Result<(), Error> {
+        let (p, n) = experts.map_or((std::ptr::null(), -1), |e| (e.as_ptr(), e.len() as c_int));
+        self.ok(unsafe { ffi::moe_st_load_moe_layer(self.st, tier.ctx, l as c_int, tl as c_int, p, n) })
+    }
+    pub fn load_model(&self, m: &mut GpuModel) -> Result<(), Error> {
+        self.ok(unsafe { ffi::moe_st_load_model(self.st, m.m) })
+    }
+}
+
+impl Drop for Weights {
+    fn drop(&mut self) {
+        unsafe { ffi::moe_st_close(self.st) }
+    }
+}
+
+/// placement.json (main.rs:455): the expert ids of (layer, tier) in slot order.
+pub fn placement(path: &str, layer: usize, tier: usize) -> Result<Vec<i32>, Error> {
+    let c = std::ffi::CString::new(path).map_err(|_| Error { code: -1, msg: "NUL in path".into() })?;
+    let mut n: c_int = 0;
+    let err = || cstr(unsafe { ffi::moe_st_last_error(std::ptr::null()) });
+    check(unsafe { ffi::moe_placement_read(c.as_ptr(), layer as c_int, tier as c_int, std::ptr::null_mut(), 0, &mut n) }, err)?;
+    let mut ids = vec![0i32; n as usize];
+    check(unsafe { ffi::moe_placement_read(c.as_ptr(), layer as c_int, tier as c_int, ids.as_mut_ptr(), n, &mut n) }, err)?;
+    Ok(ids)
 }

@@ -1,8 +1,9 @@
 /*
  * cpu_moe_port.c — AVX-512 BF16 + OpenMP port of solar_hybrid/cpu_moe.cpp:38-96 (the CPU baseline "port").
  *
- * TEST/BENCH INFRASTRUCTURE ONLY: timed by the benchmark's cpu_baseline leg when the reference's own cpu_kern.c build
- * (oracle/_ref) is unavailable; checked bit-for-bit against the scalar restatement in moe_oracle.c by the tests.
+ * TEST INFRASTRUCTURE ONLY: checked bit-for-bit against the scalar restatement in moe_oracle.c by the tests (the
+ * benchmark's cpu_baseline leg times the reference's own cpu_kern.c build, oracle/_ref, or, where that cannot be loaded,
+ * the scalar restatement; it does not time this port).
  * Built into its own library with AVX-512 flags so that the scalar oracle stays loadable on any x86-64 host.
  */
 #include <math.h>
