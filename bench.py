@@ -265,10 +265,10 @@ def bench_attn(args) -> None:
         "event_ms_per_step": round(ev_us / 1e3, 5),
         "config": {"workload": "attn: GQA decode attention, 32 q / 8 kv heads, d=128, KV 4096, bf16, batch 1",
                    "n_q_heads": NQ, "n_kv_heads": NKV, "head_dim": D, "kv_len": S, "tokens": 1},
-        "roofline": {"kernel": "attn_scores + attn_pv + attn_out", "bound": "hbm", "achieved": round(achieved, 1),
+        "roofline": {"kernel": "attn_fused_kernel", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": None, "bytes_per_launch": nbytes, "avg_us": round(ev_us, 2),
-                     "timing": "timed-region hipEvents on the call's stream over the three kernels of a call"},
+                     "timing": "timed-region hipEvents on the call's stream (one kernel per call)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -260,8 +260,13 @@ int moe_rope_append_dev(int n_q_heads, int n_kv_heads, int head_dim, uint16_t* q
  *   sc[t] = bf16(bf16(q_h . k_t) * scale)  (dot summed left to right in fp32: bit-identical scores),
  *   p[t] = bf16(exp(sc[t] - max sc) / sum exp(sc - max sc)),  out_h = bf16(sum_t p[t] v_t)  (fp32 sums in the GPU's order).
  * q [NQ, D] bf16 (after RoPE), k_cache / v_cache [S, NKV, D] bf16 (16-byte aligned), out [NQ, D] bf16; D = 128,
- * NQ = G * NKV with G in {1, 2, 4, 8}.  Device pointers; enqueued on `stream` (NULL: the null stream), not synchronised.  The
- * caller passes a device workspace of moe_attn_workspace_bytes() (scores, then per-chunk partials). */
+ * NQ = G * NKV with G in {1, 2, 4, 8}, 1 <= S <= 65536.  Device pointers; enqueued on `stream` (NULL: the null
+ * stream), not synchronised; one kernel launch, which may be captured in a HIP graph and replayed.  The caller
+ * passes a device workspace of moe_attn_workspace_bytes() bytes (0 for arguments out of range) dedicated to these
+ * calls, zero-filled before its first call: a 256-byte header (the call counter), the call's scores ([NQ, S] fp32
+ * from byte 256, left there for the caller), then tagged per-chunk statistics and partials.  Between calls nothing
+ * else may write it (zeroing all of it again is allowed).  Pass the same workspace_bytes on every call on a
+ * workspace.  Calls that share a workspace and overlap in time (two streams) race. */
 size_t moe_attn_workspace_bytes(int n_q_heads, int head_dim, int S);
 int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
                         const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
@@ -270,9 +275,10 @@ const char* moe_attn_last_error(void); /* message of this thread's last failed m
 
 /* Allocation-free variant of moe_attn_decode_dev.  No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
- * scores and partials live in a file-scope device array of moe_attn_noalloc_max_bytes() bytes (4 MiB: 64 query heads
- * x 8192 positions), one per GPU, held until the process ends; its address is looked up once per device.  The call
- * allocates nothing; it returns MOE_GPU_EINVAL, enqueueing nothing, when moe_attn_workspace_bytes(n_q_heads,
+ * workspace lives in a file-scope device array of moe_attn_noalloc_max_bytes() bytes (6.3 MB: 64 query heads x 8192
+ * positions), one per GPU, held until the process ends; its address is looked up once per device.  The call
+ * allocates nothing (its first call on a device also enqueues the clearing of the array: make that call outside a
+ * graph capture); it returns MOE_GPU_EINVAL, enqueueing nothing, when moe_attn_workspace_bytes(n_q_heads,
  * head_dim, S) exceeds that size.  Outputs are bit-identical to moe_attn_decode_dev's.  All calls on one GPU share
  * its array: calls that overlap on one GPU (two streams, two threads) race; serialise them on one stream. */
 size_t moe_attn_noalloc_max_bytes(void);

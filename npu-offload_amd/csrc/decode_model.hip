@@ -225,6 +225,8 @@ int moe_model_create(int device, const moe_model_config* cfg, moe_model** out) {
         return bail(rc);
     m->attn_ws_bytes = moe_attn_workspace_bytes(c.n_q_heads, c.head_dim, c.max_ctx);
     if ((rc = alloc(m, &m->attn_ws, m->attn_ws_bytes, "attention workspace"))) return bail(rc);
+    if (hipMemset(m->attn_ws, 0, m->attn_ws_bytes) != hipSuccess)  // the attention workspace starts zero-filled
+        return bail(mfail(m, MOE_GPU_EHIP, "hipMemset of the attention workspace failed"));
     if (hipHostMalloc((void**)&m->h_tok, 8, hipHostMallocDefault) != hipSuccess)
         return bail(mfail(m, MOE_GPU_ENOMEM, "hipHostMalloc failed"));
     if (hipMemsetAsync(m->d_bad, 0, 4, m->stream) != hipSuccess || hipStreamSynchronize(m->stream) != hipSuccess)

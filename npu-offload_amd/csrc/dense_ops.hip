@@ -26,10 +26,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // y[m] = bf16(sum_k W[m, k] x[k]) for one token: x staged in LDS; waves take steps of RB whole rows, CG 16-byte
 // chunks per lane per load group, the next group's loads issued before the step's butterfly (the LM head's scheme).
+// The first group's weight loads are issued before x is staged, so the staging round trip overlaps them.
 // norm_w != null: x is the residual stream and the GEMV reads rmsnorm(x, norm_w) (host.rs:71-76: ms = sum(x^2) / K in
-// fp32, r = 1 / sqrt(ms + eps), h = bf16(bf16(x * r) * w)), which every workgroup computes into LDS (the squares summed
-// per thread over its strided elements, then a 64-lane butterfly, then the 4 wavefronts in order): the layer's input
-// norm folded into its q|k|v projection.
+// fp32, r = 1 / sqrt(ms + eps), h = bf16(bf16(x * r) * w)), which every workgroup computes into LDS (each thread's
+// 16-byte chunks of x and of the weight loaded at once; the squares summed per thread over its chunks in order, then a
+// 64-lane butterfly, then the 4 wavefronts in order): the layer's input norm folded into its q|k|v projection.
+constexpr int kXC = 4;  // 16-byte chunks of x per thread per staging pass (one pass for K <= 8192)
 template <int RB, int CG>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ y, int M, int K,
@@ -37,23 +39,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     extern __shared__ __align__(16) uint16_t xs[];
     __shared__ float red[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    if (norm_w) {
-        float s = 0.f;
-        for (int i = tid; i < K; i += 256) {
-            const float v = bf2f(x[i]);
-            s = fmaf(v, v, s);
-        }
-        s = wave_sum(s);
-        if (lane == 0) red[wv] = s;
-        __syncthreads();
-        const float ms = (red[0] + red[1] + red[2] + red[3]) / (float)K;
-        const float r = 1.0f / sqrtf(ms + eps);
-        for (int i = tid; i < K; i += 256) xs[i] = (uint16_t)f2bf(bf2f(f2bf(bf2f(x[i]) * r)) * bf2f(norm_w[i]));
-    } else {
-        for (int i = tid * 8; i < K; i += 256 * 8)
-            *reinterpret_cast<u32x4*>(&xs[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
-    }
-    __syncthreads();
     const int nch = K / 512;
     const int gw = blockIdx.x * kWaves + wv, nw = gridDim.x * kWaves;
     u32x4 wq[RB][CG];
@@ -71,6 +56,68 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     };
     int r0 = gw * RB, c0 = 0;
     if (r0 < M) load_group(r0, 0);
+    // stage x (normalised when norm_w): thread tid holds 16-byte chunks tid + 256 j
+    const int nc = K / 8;
+    const u32x4* x4 = reinterpret_cast<const u32x4*>(x);
+    const u32x4* w4 = reinterpret_cast<const u32x4*>(norm_w);
+    float rs = 1.f;
+    if (norm_w) {
+        float s = 0.f;
+        for (int j0 = 0; j0 < nc; j0 += 256 * kXC) {
+            u32x4 xv[kXC];
+#pragma unroll
+            for (int j = 0; j < kXC; ++j)
+                if (j0 + 256 * j + tid < nc) xv[j] = x4[j0 + 256 * j + tid];
+#pragma unroll
+            for (int j = 0; j < kXC; ++j) {
+                if (j0 + 256 * j + tid < nc) {
+                    const uint32_t e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float lo = bf2f(e4[i] & 0xFFFFu), hi = bf2f(e4[i] >> 16);
+                        s = fmaf(lo, lo, s);
+                        s = fmaf(hi, hi, s);
+                    }
+                }
+            }
+        }
+        s = wave_sum(s);
+        if (lane == 0) red[wv] = s;
+        __syncthreads();
+        const float ms = (((red[0] + red[1]) + red[2]) + red[3]) / (float)K;
+        rs = 1.0f / sqrtf(ms + eps);
+    }
+    for (int j0 = 0; j0 < nc; j0 += 256 * kXC) {
+        u32x4 xv[kXC], nv[kXC];
+#pragma unroll
+        for (int j = 0; j < kXC; ++j) {
+            if (j0 + 256 * j + tid < nc) {
+                xv[j] = x4[j0 + 256 * j + tid];
+                if (norm_w) nv[j] = w4[j0 + 256 * j + tid];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kXC; ++j) {
+            const int c = j0 + 256 * j + tid;
+            if (c < nc) {
+                u32x4 o = xv[j];
+                if (norm_w) {
+                    const uint32_t e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                    const uint32_t n4[4] = {nv[j].x, nv[j].y, nv[j].z, nv[j].w};
+                    uint32_t r4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t lo = f2bf(bf2f(f2bf(bf2f(e4[i] & 0xFFFFu) * rs)) * bf2f(n4[i] & 0xFFFFu));
+                        const uint32_t hi = f2bf(bf2f(f2bf(bf2f(e4[i] >> 16) * rs)) * bf2f(n4[i] >> 16));
+                        r4[i] = lo | (hi << 16);
+                    }
+                    o = u32x4{r4[0], r4[1], r4[2], r4[3]};
+                }
+                *reinterpret_cast<u32x4*>(&xs[8 * c]) = o;
+            }
+        }
+    }
+    __syncthreads();
     while (r0 < M) {
 #pragma unroll
         for (int c = 0; c < CG; ++c) {

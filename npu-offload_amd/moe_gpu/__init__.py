@@ -519,6 +519,16 @@ def attn_workspace_bytes(n_q_heads: int, S: int, head_dim: int = 128) -> int:
     return int(load_library().moe_attn_workspace_bytes(n_q_heads, head_dim, S))
 
 
+ATTN_SCORES_OFFSET = 256  # bytes: the workspace's header, then the last call's scores [NQ, S] fp32
+
+
+def attn_scores(workspace, n_q_heads: int, S: int):
+    """The scores [NQ, S] (fp32) of the last attn_decode_dev call on `workspace`, as a view of it."""
+    f = workspace.view(-1).view(dtype=__import__("torch").float32)
+    o = ATTN_SCORES_OFFSET // 4
+    return f[o:o + n_q_heads * S].view(n_q_heads, S)
+
+
 def gemv_norm_dev(W, x, norm_w, y, eps: float = 1e-5, stream=None) -> None:
     """y = bf16(W . rmsnorm(x, norm_w)) on device tensors (the input norm folded into the q|k|v projection)."""
     M, K = W.shape

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from moe_gpu import EINVAL, MoeGpuError, attn_decode_dev, attn_workspace_bytes
+from moe_gpu import EINVAL, MoeGpuError, attn_decode_dev, attn_scores, attn_workspace_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -34,7 +34,7 @@ def run_gpu(q, k, v, NKV, S=None):
     torch.cuda.synchronize()
     attn_decode_dev(qd, kd, vd, od, ws, NQ, NKV, S)  # null stream: ordered after torch's copies
     torch.cuda.synchronize()
-    return od.cpu().numpy().view(np.uint16), ws[:NQ * S].cpu().numpy().reshape(NQ, S)
+    return od.cpu().numpy().view(np.uint16), attn_scores(ws, NQ, S).cpu().numpy()
 
 
 def check_out(gpu, ref):
@@ -55,6 +55,76 @@ def test_attention_matches_oracle(NQ, NKV, S):
     out, gsc = run_gpu(q, k, v, NKV)
     np.testing.assert_array_equal(gsc.view(np.uint32), sc.view(np.uint32))
     check_out(out, ref)
+
+
+@pytest.mark.parametrize("NQ,NKV,S", [(32, 8, 4096), (16, 2, 1000), (8, 8, 300)])
+def test_attention_fallback_paths_same_bits(NQ, NKV, S, monkeypatch):
+    """MOE_ATTN_POLL=0 ends every wait for another workgroup's words at once, so workgroups compute missing chunk
+    statistics and partials themselves: the output and scores must not change by a bit."""
+    say(f"attention fallback NQ={NQ} NKV={NKV} S={S}")
+    rng = np.random.default_rng(S + 11)
+    q = O.f2bf(rng.standard_normal((NQ, 128)).astype(np.float32))
+    k = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    out, sc = run_gpu(q, k, v, NKV)
+    monkeypatch.setenv("MOE_ATTN_POLL", "0")
+    out0, sc0 = run_gpu(q, k, v, NKV)
+    monkeypatch.delenv("MOE_ATTN_POLL")
+    np.testing.assert_array_equal(out0, out)
+    np.testing.assert_array_equal(sc0.view(np.uint32), sc.view(np.uint32))
+
+
+def test_attention_longest_context():
+    """S = 65536 (the maximum): more workgroups than fit on the chip at once, so each takes several chunks."""
+    NQ, NKV, S = 32, 8, 65536
+    say(f"attention NQ={NQ} NKV={NKV} S={S}")
+    rng = np.random.default_rng(9)
+    q = O.f2bf(rng.standard_normal((NQ, 128)).astype(np.float32))
+    k = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    ref, sc = O.attention(q, k, v, NKV)
+    out, gsc = run_gpu(q, k, v, NKV)
+    np.testing.assert_array_equal(gsc.view(np.uint32), sc.view(np.uint32))
+    check_out(out, ref)
+
+
+def test_attention_graph_replays():
+    """One call captured in a HIP graph and replayed with new q, eager calls on the same workspace in between: the
+    epochs live in the workspace, so every replay and every eager call gets a fresh one and the same bits."""
+    import torch
+
+    NQ, NKV, S = 32, 8, 1000
+    say(f"attention graph replays NQ={NQ} NKV={NKV} S={S}")
+    dev = "cuda:0"
+    rng = np.random.default_rng(21)
+    k = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    kd = torch.from_numpy(k.view(np.int16)).to(dev)
+    vd = torch.from_numpy(v.view(np.int16)).to(dev)
+    qd = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    od = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    oe = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    ws = torch.zeros(attn_workspace_bytes(NQ, S) // 4, dtype=torch.float32, device=dev)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    attn_decode_dev(qd, kd, vd, od, ws, NQ, NKV, S, stream=s)  # first call on the workspace: outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        attn_decode_dev(qd, kd, vd, od, ws, NQ, NKV, S, stream=s)
+    torch.cuda.synchronize()
+    for r in range(4):
+        q = O.f2bf(rng.standard_normal((NQ, 128)).astype(np.float32))
+        qd.copy_(torch.from_numpy(q.view(np.int16)).to(dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = od.cpu().numpy().view(np.uint16).copy()
+        attn_decode_dev(qd, kd, vd, oe, ws, NQ, NKV, S, stream=s)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got, oe.cpu().numpy().view(np.uint16))
+        ref, _ = O.attention(q, k, v, NKV)
+        check_out(got, ref)
 
 
 def test_attention_one_hot_exact():
@@ -78,7 +148,7 @@ def test_attention_errors():
 
     ws = torch.zeros(1024, dtype=torch.float32, device="cuda:0")
     x = torch.zeros(4096, dtype=torch.int16, device="cuda:0")
-    for args in ((32, 8, 64, 16), (32, 5, 128, 16), (32, 2, 128, 16), (32, 8, 128, 0), (32, 8, 128, 4096)):
+    for args in ((32, 8, 64, 16), (32, 5, 128, 16), (32, 2, 128, 16), (32, 8, 128, 0), (32, 8, 128, 4096), (32, 8, 128, 65537)):
         NQ, NKV, D, S = args
         with pytest.raises(MoeGpuError) as e:
             attn_decode_dev(x, x, x, x, ws, NQ, NKV, S, head_dim=D)

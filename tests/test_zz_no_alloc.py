@@ -47,7 +47,7 @@ def test_noalloc_refuses_sizes_beyond_its_scratch():
     L = load_library()
     cap = L.moe_attn_noalloc_max_bytes()
     assert cap > 0
-    S_big = 1 << 20  # 64 heads x 2^20 positions of fp32 scores is far beyond the scratch
+    S_big = 1 << 16  # the longest context: 64 heads x 65536 positions need 84 MB, beyond the scratch
     say("noalloc attention refuses an oversize call")
     rc = L.moe_attn_decode_noalloc_dev(64, 8, 128, S_big, 0.088, 16, 16, 16, 16, None)
     assert rc == EINVAL
