@@ -363,12 +363,15 @@ int run_layer(moe_gpu* c, int layer, int T, const moe::StageSrc& in, int32_t* id
     a.gpart = c->d_gpart;
     if ((rc = next_epoch(c, &a.epoch))) return rc;
     a.err = &c->d_sync->err;
-    if (c->fused && T <= 8) {  // 9 to 16 tokens run the unfused kernels (the same arithmetic)
+    // Up to 7 tokens: the fused kernel.  8 or more (the batch >= 8 grouped case): the unfused kernels, whose cores for
+    // units of more than 4 tokens use MFMA (measured at Solar batch 8: 205 us against the fused kernel's 211 us, whose
+    // registers have no room for the MFMA cores).
+    if (c->fused && T < 8) {
         FusedArgs f;
         f.e = a;
         f.logits = c->d_logits_tag;
         f.sync = c->d_sync;
-        f.nR = do_topk ? (c->d.E + moe::kRouterRows - 1) / moe::kRouterRows : 0;
+        f.nR = do_topk ? moe::router_units(c->d.E, T) : 0;
         f.do_topk = do_topk ? 1 : 0;
         f.rule = c->route_rule;
         f.router_poll = c->router_poll;
@@ -892,7 +895,7 @@ int moe_gpu_trace_units(moe_gpu* c, int on) {
     int rc = enter(c);
     if (rc) return rc;
     if (on && !c->d_trace) {
-        const size_t units = (size_t)moe::fused_units((c->d.E + moe::kRouterRows - 1) / moe::kRouterRows,
+        const size_t units = (size_t)moe::fused_units(moe::router_units(c->d.E, c->d.max_t),
                                                       c->d.n_shared + c->d.max_t * c->d.k, c->d.n_shared, c->d.F,
                                                       c->d.H, moe::kMaxKp, moe::kMaxKp);
         const size_t bytes = units * moe::kTraceFields * sizeof(uint64_t);

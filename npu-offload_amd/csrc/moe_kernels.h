@@ -20,6 +20,13 @@ constexpr int kMaxSlots = kMaxShared + kMaxTokens * kMaxTopk;
 #define MOE_ROUTER_ROWS 8
 #endif
 constexpr int kRouterRows = MOE_ROUTER_ROWS;  // router rows per router unit (2, 4 or 8): two per wavefront
+constexpr int kRouterTG = 2;                  // tokens per router unit when a call has several
+// Router units of a call: row groups of kRouterRows, times token groups of kRouterTG when T > 1 (unit u: row group
+// u % row groups, token group u / row groups).
+inline int router_units(int E, int T) {
+    const int nrg = (E + kRouterRows - 1) / kRouterRows;
+    return T > 1 ? nrg * ((T + kRouterTG - 1) / kRouterTG) : nrg;
+}
 
 // Routing rules of the compute calls (the flag bits MOE_GPU_ROUTE_* of the C ABI select them).
 enum RouteRule { kRouteSoftmax = 0, kRouteSigmoid = 1 };

@@ -287,6 +287,129 @@ __device__ __forceinline__ void reduce_waves(lds_float* red, const float* acc, i
 }
 
 // --------------------------------------------------------------------------------------------------------------------
+// MFMA path of the batch >= 8 grouped case (a call of 8 or more tokens, units with more than 4 tokens): the tile's
+// 64 rows x up to 8 tokens as 4 row blocks of v_mfma_f32_16x16x32_bf16 (16 rows x 16 token columns x 32 k; columns
+// of tokens past the unit's count are computed from token 0's activations and dropped).  Operand layout (checked on
+// the device): lane l holds A row l % 16 and B column l % 16 over k = 8 (l / 16) .. 8 (l / 16) + 7; D rows
+// 4 (l / 16) .. 4 (l / 16) + 3 of column l % 16.  The tile layout [chunk][64 rows] of 16-byte chunks gives each lane
+// its A operand in one 16-byte load (row 16 b + l % 16 of chunk c + l / 16); its B operand is one LDS read of the
+// token's activation chunk.  The sums run in the MFMA's order, not the dot2 chains', so this path matches the
+// others within the layer bars rather than bit for bit.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma_bf16(u32x4 a, u32x4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+}
+
+// Chunks [c0, c1) of a 64-row tile in groups of 4 (bf16: 8 k per chunk, one MFMA per row block; int8: 16 k per chunk,
+// two MFMAs per row block, the weights widened to bf16 exactly).  Two banks of MF_DEPTH groups alternate as in
+// TileStream; lanes whose chunk lies past c1 (the last group) load zeros.
+#ifndef MOE_MF_DEPTH
+#define MOE_MF_DEPTH 2
+#endif
+template <bool Q8>
+struct MfmaStream {
+    static constexpr int D = MOE_MF_DEPTH;
+    const u32x4* p;  // tile + (lane / 16) * 64 + lane % 16
+    int c0, c1;
+    u32x4 A[D][4];
+    __device__ __forceinline__ void load(u32x4 (&bank)[D][4], int c) {
+        const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            const bool ok = c + 4 * u + g < c1;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                bank[u][b] = ok ? ld_stream(p + (size_t)(c + 4 * u) * 64 + 16 * b) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    __device__ __forceinline__ void consume(const u32x4 (&bank)[D][4], int c, const lds_u32x4* xs, int xo,
+                                            f32x4_t (&d)[4]) {
+        const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            const int cc = min(c + 4 * u + g, c1 - 1);  // past c1: a valid chunk, its A operand is zero
+            if (!Q8) {
+                const u32x4 x = xs[xo + cc];
+#pragma unroll
+                for (int b = 0; b < 4; b++) d[b] = mfma_bf16(bank[u][b], x, d[b]);
+            } else {
+                const u32x4 x0 = xs[xo + 2 * cc], x1 = xs[xo + 2 * cc + 1];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    unsigned w[8];
+                    i8x4_to_bf16(bank[u][b].x, w[0], w[1]);
+                    i8x4_to_bf16(bank[u][b].y, w[2], w[3]);
+                    i8x4_to_bf16(bank[u][b].z, w[4], w[5]);
+                    i8x4_to_bf16(bank[u][b].w, w[6], w[7]);
+                    d[b] = mfma_bf16(u32x4{w[0], w[1], w[2], w[3]}, x0, d[b]);
+                    d[b] = mfma_bf16(u32x4{w[4], w[5], w[6], w[7]}, x1, d[b]);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void begin(const u32x4* __restrict__ tile, int c0_, int c1_) {
+        const int lane = threadIdx.x & 63;
+        p = tile + (lane >> 4) * 64 + (lane & 15);
+        c0 = c0_;
+        c1 = c1_;
+        if (c1 > c0) load(A, c0);
+    }
+    __device__ __forceinline__ void run(const lds_u32x4* xs, int xo, f32x4_t (&d)[4]) {
+        u32x4 B[D][4];
+        const int step = 4 * D, nb = (c1 - c0 + step - 1) / step;
+        int b = 0;
+        for (; b + 2 < nb; b += 2) {
+            load(B, c0 + (b + 1) * step);
+            consume(A, c0 + b * step, xs, xo, d);
+            load(A, c0 + (b + 2) * step);
+            consume(B, c0 + (b + 1) * step, xs, xo, d);
+        }
+        if (nb - b == 2) {
+            load(B, c0 + (b + 1) * step);
+            consume(A, c0 + b * step, xs, xo, d);
+            consume(B, c0 + (b + 1) * step, xs, xo, d);
+        } else if (nb - b == 1) {
+            consume(A, c0 + b * step, xs, xo, d);
+        }
+    }
+};
+
+// This lane's token column l % 16 as an activation chunk offset: slot token (l % 16) if it exists, else token 0's.
+// (masks and ors, not selects: a select chain over the array compiled to a scratch-memory table lookup)
+template <int NT>
+__device__ __forceinline__ int mfma_xoff(const int* xoff, int ntok) {
+    const int j = threadIdx.x & 15, jj = j < ntok ? j : 0;
+    int xo = 0;
+#pragma unroll
+    for (int i = 0; i < NT; i++) xo |= xoff[i] & -(int)(jj == i);
+    return xo;
+}
+
+// The MFMA partials of the 4 wavefronts into red[(wave * NT + j) * 64 + row], then summed as reduce_waves does.
+template <int NT>
+__device__ __forceinline__ void reduce_waves_mfma(lds_float* red, const f32x4_t (&d)[4], int ntok) {
+    const int wave = wave_id(), lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    if (j < NT && j < ntok) {
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * NT + j) * 64 + 16 * b + 4 * g + r] = d[b][r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int jj = 0; jj < NT; jj++)
+            if (jj < ntok)
+                red[jj * 64 + lane] = ((red[jj * 64 + lane] + red[(NT + jj) * 64 + lane]) + red[(2 * NT + jj) * 64 + lane]) +
+                                      red[(3 * NT + jj) * 64 + lane];
+    }
+    __syncthreads();
+}
+
+// --------------------------------------------------------------------------------------------------------------------
 // Dynamic shared-memory plan of a workgroup (16-byte aligned pieces):
 //   xs    [T][H/8] u32x4      all tokens' activations, staged once per workgroup
 //   as    [NT][F/8] u32x4     one slot's act rows (down units)
@@ -443,11 +566,12 @@ __device__ __forceinline__ void combine_store(const ExpertArgs& a, size_t o, flo
 // wave w < kRouterRows / 2 computes rows e0 + 2w (lanes 0-31) and e0 + 2w + 1 (lanes 32-63) for all T tokens.
 // stage: the activations (from src) are staged once the weight loads are in flight.  src travels by value: an
 // address of a kernel argument would make the compiler copy the arguments to scratch memory.
+// Several tokens: a unit takes kRouterTG of them (tokens t0 ..), so that T tokens spread over more workgroups.
 template <int NT>
 __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __restrict__ wr, int e0, int E, int H, int T,
                                             uint64_t* __restrict__ logits, float* __restrict__ logits_out,
                                             unsigned epoch, bool stage, const StageSrc src, bool stamp,
-                                            uint64_t& t_in, uint64_t& t_dot) {
+                                            uint64_t& t_in, uint64_t& t_dot, int t0 = 0) {
     static_assert(kRouterRows == 2 || kRouterRows == 4 || kRouterRows == 8, "two router rows per wavefront");
     const int wave = wave_id(), lane = threadIdx.x & 63;
     if (2 * wave >= kRouterRows) {  // a wavefront without rows only takes part in the staging
@@ -458,8 +582,8 @@ __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __rest
     float acc[NT];
     const u32x4* w = reinterpret_cast<const u32x4*>(wr);
     const size_t rs = (size_t)H / 8;  // u32x4 per row
-    ck_rows_dot_chain<NT>(w + (size_t)min(ea, E - 1) * rs, w + (size_t)min(ea + 1, E - 1) * rs, H, T,
-                          (const LDS_AS unsigned*)s.xs, NT == 1 ? s.xf : nullptr, acc,
+    ck_rows_dot_chain<NT>(w + (size_t)min(ea, E - 1) * rs, w + (size_t)min(ea + 1, E - 1) * rs, H, T - t0,
+                          (const LDS_AS unsigned*)s.xs + (size_t)t0 * (H / 2), NT == 1 ? s.xf : nullptr, acc,
                           [&]() __attribute__((always_inline)) {
                               if (stage) stage_in(s, src, T, H);
                               if (stamp) t_in = __builtin_amdgcn_s_memrealtime();
@@ -468,9 +592,9 @@ __device__ __forceinline__ void router_unit(const Lds& s, const uint16_t* __rest
     if ((lane & 31) == 0 && e < E) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < T) {
-                st_tag(&logits[(size_t)t * E + e], epoch, __float_as_uint(acc[t]));
-                if (logits_out) logits_out[(size_t)t * E + e] = acc[t];
+            if (t0 + t < T) {
+                st_tag(&logits[(size_t)(t0 + t) * E + e], epoch, __float_as_uint(acc[t]));
+                if (logits_out) logits_out[(size_t)(t0 + t) * E + e] = acc[t];
             }
         }
     }
@@ -514,6 +638,32 @@ __device__ __forceinline__ float sigmoid_ref(float v) {
     return 1.f / (1.f + ex);
 }
 
+// The largest of the wave's 64-bit keys, in every lane: DPP moves within rows of 16 lanes (each step combining equal
+// halves), then the four rows' maxima.  All 64 lanes must be active.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#define MOE_DPP_MAX_STEP(CTRL)                                                                             \
+    {                                                                                                      \
+        const unsigned lo_ = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)v, CTRL, 0xF, 0xF, false);  \
+        const unsigned hi_ = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)(v >> 32), CTRL, 0xF, 0xF, false); \
+        const uint64_t o_ = ((uint64_t)hi_ << 32) | lo_;                                                   \
+        v = o_ > v ? o_ : v;                                                                               \
+    }
+    MOE_DPP_MAX_STEP(0xB1)   // quad [1,0,3,2]
+    MOE_DPP_MAX_STEP(0x4E)   // quad [2,3,0,1]
+    MOE_DPP_MAX_STEP(0x141)  // row half mirror
+    MOE_DPP_MAX_STEP(0x140)  // row mirror
+#undef MOE_DPP_MAX_STEP
+    uint64_t m = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 16 * r);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 16 * r);
+        const uint64_t x = ((uint64_t)hi << 32) | lo;
+        m = x > m ? x : m;
+    }
+    return m;
+}
+
 // Top-k and expert grouping into rt.  Selection: the k largest keys (score descending, index ascending); each thread
 // counts, for one (token, expert) and a slice of the experts, how many keys beat it (its rank), reading the keys as
 // shared-memory broadcasts, so the whole workgroup works on it.  Scores and gates by rule:
@@ -526,6 +676,8 @@ __device__ __forceinline__ float sigmoid_ref(float v) {
 // scr: kRouteScratchBytes of LDS.  poll >= 0 bounds the wait for the tagged logits to that many passes: the call then
 // returns 1, uniformly, when logits are still missing (their router units have not run), and the caller computes
 // them itself and calls again; poll < 0 waits up to the launch-wide limit.  Returns 0 once rt is complete.
+// MULTI false: the caller only ever has one token (the several-token selection is left out of its code).
+template <bool MULTI = true>
 __device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned char* scr,
                                            const uint64_t* __restrict__ logits, unsigned epoch, unsigned* err,
                                            const float* __restrict__ bias, const int32_t* ids_in,
@@ -571,9 +723,36 @@ __device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned cha
                     if (!(v == v)) v = -INFINITY;
                     if (v == 0.f) v = 0.f;  // -0 and +0 compare equal: one key
                     keys[i] = route_key(v, i % E);
+                    if (MULTI && T > 1) ((LDS_AS float*)cnt)[i] = sg[m];
                 }
             }
             __syncthreads();
+            if (MULTI && T > 1 && E <= 4 * 64) {
+                // 2'. several tokens: one wavefront per token takes the k largest keys one by one (a key's expert index
+                //     makes every key distinct, so this is the same selection as counting ranks below), lane l holding
+                //     the keys of experts l, l + 64, ...; the taken key is zeroed (every real key is nonzero)
+                const int wave = wave_id(), lane = tid & 63;
+                for (int tl = wave; tl < nt; tl += nthr / 64) {
+                    const int t = t0 + tl;
+                    uint64_t kk[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) kk[q] = lane + 64 * q < E ? keys[tl * E + lane + 64 * q] : 0ull;
+                    for (int r = 0; r < k; r++) {
+                        const uint64_t best = max(max(kk[0], kk[1]), max(kk[2], kk[3]));
+                        const uint64_t top = wave_max_u64(best);
+                        const int e = (int)~(unsigned)top;
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            if (kk[q] == top) kk[q] = 0ull;
+                        if (lane == 0) {
+                            rt->id[t * k + r] = e;
+                            rt->gate[t * k + r] =
+                                rule == kRouteSigmoid ? ((const LDS_AS float*)cnt)[tl * E + e] : route_key_score(top);
+                        }
+                    }
+                }
+                __syncthreads();
+            } else {
             // 2. ranks: work item (part p, item i) counts the keys of experts [p E / parts, (p + 1) E / parts) above
             //    key i; parts spread a small pass over the whole workgroup
             int parts = 1;  // a power of two dividing E
@@ -612,6 +791,7 @@ __device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned cha
                 }
             }
             __syncthreads();
+            }
             // 4. gates, one wavefront per token, lane r holding rank r
             const int wave = wave_id(), lane = tid & 63;
             for (int tl = wave; tl < nt; tl += nthr / 64) {
@@ -790,7 +970,7 @@ __device__ __forceinline__ void route_publish(const lds_RouteTab* rt, int T, int
 // the slot's tokens.  Sums: wavefronts in order within a part, then parts in order.  Parts below kp - 1 publish their
 // partial sums to gpart; part kp - 1 (the tile's last unit in queue order) reads them back, finishes the tile and
 // publishes act.  pair0: the slot's first (slot, token) pair, indexing gpart.
-template <int N, bool Q8OK>
+template <int N, bool Q8OK, bool MF = false>
 __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
                                             const int* tok, int pair0, uint64_t& stamp) {
     const int H = a.d.H, F = a.d.F, kp = e < 0 ? a.kps : a.kp, ntile = F / 32;
@@ -799,23 +979,47 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
     int xoff[N];
 #pragma unroll
     for (int j = 0; j < N; j++) xoff[j] = j < ntok ? tok[j] * nc : 0;
-    float acc[N];
-#pragma unroll
-    for (int j = 0; j < N; j++) acc[j] = 0.f;
     const bool q8 = Q8OK && a.int8 && e >= 0;  // Q8OK false: no int8 code in this instantiation
-    if (!q8) {
-        const uint16_t* base =
-            e >= 0 ? a.L.gu + (size_t)e * a.d.gu_stride() : a.L.sgu + (size_t)(-1 - e) * a.d.gu_stride();
-        const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)tile * nc * 64;
-        const int cpw = nc / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
-        tile_stream<N, false>(t, c0, c0 + cpw, s.xs, xoff, acc);
+    if constexpr (MF) {
+        f32x4_t d[4] = {};
+        const int xo = mfma_xoff<N>(xoff, ntok);
+        if (!q8) {
+            const uint16_t* base =
+                e >= 0 ? a.L.gu + (size_t)e * a.d.gu_stride() : a.L.sgu + (size_t)(-1 - e) * a.d.gu_stride();
+            const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)tile * nc * 64;
+            const int cpw = nc / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+            MfmaStream<false> ms;
+            ms.begin(t, c0, c0 + cpw);
+            ms.run(s.xs, xo, d);
+        } else {
+            const int ncq = H / 16;
+            const u32x4* t =
+                reinterpret_cast<const u32x4*>(a.L.gu_q8 + (size_t)e * a.d.gu_stride()) + (size_t)tile * ncq * 64;
+            const int cpw = ncq / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+            MfmaStream<true> ms;
+            ms.begin(t, c0, c0 + cpw);
+            ms.run(s.xs, xo, d);
+        }
+        reduce_waves_mfma<N>(s.red, d, ntok);
     } else {
-        const int ncq = H / 16;
-        const u32x4* t = reinterpret_cast<const u32x4*>(a.L.gu_q8 + (size_t)e * a.d.gu_stride()) + (size_t)tile * ncq * 64;
-        const int cpw = ncq / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
-        tile_stream<N, true>(t, c0, c0 + cpw, s.xs, xoff, acc);
+        float acc[N];
+#pragma unroll
+        for (int j = 0; j < N; j++) acc[j] = 0.f;
+        if (!q8) {
+            const uint16_t* base =
+                e >= 0 ? a.L.gu + (size_t)e * a.d.gu_stride() : a.L.sgu + (size_t)(-1 - e) * a.d.gu_stride();
+            const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)tile * nc * 64;
+            const int cpw = nc / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+            tile_stream<N, false>(t, c0, c0 + cpw, s.xs, xoff, acc);
+        } else {
+            const int ncq = H / 16;
+            const u32x4* t =
+                reinterpret_cast<const u32x4*>(a.L.gu_q8 + (size_t)e * a.d.gu_stride()) + (size_t)tile * ncq * 64;
+            const int cpw = ncq / (kWaves * kp), c0 = (kpi * kWaves + wave) * cpw;
+            tile_stream<N, true>(t, c0, c0 + cpw, s.xs, xoff, acc);
+        }
+        reduce_waves<N>(s.red, acc, N);
     }
-    reduce_waves<N>(s.red, acc, N);
     if (wave == 0) {
         uint64_t* gp0 = a.gpart + (((size_t)pair0 * ntile + tile) * kMaxKp) * 64 + lane;  // + (j*ntile*kMaxKp + q)*64
         if (kpi < kp - 1) {
@@ -858,14 +1062,21 @@ __device__ __forceinline__ void gateup_core(const Lds& s, const ExpertArgs& a, i
     __syncthreads();  // s.red is reused by the next unit
 }
 
-template <int NT, bool Q8OK = true>
+// MFOK: the MFMA cores may be used (the unfused kernels; the fused kernel's register budget has no room for them).
+template <int NT, bool Q8OK = true, bool MFOK = false>
 __device__ __forceinline__ void gateup_unit(const Lds& s, const ExpertArgs& a, int sl, int tile, int kpi, int e, int ntok,
                                             const int* tok, int pair0, uint64_t& stamp) {
     if (ntok <= 1 || NT == 1) gateup_core<1, Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
     else if (ntok <= 2 || NT == 2) gateup_core<(NT < 2 ? NT : 2), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
     else if (ntok <= 4 || NT == 4) gateup_core<(NT < 4 ? NT : 4), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else if (ntok <= 8 || NT == 8) gateup_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
-    else gateup_core<NT, Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    else if (ntok <= 8 || NT == 8) {
+        if (MFOK && NT >= 8 && a.T >= 8)  // the batch >= 8 grouped case: MFMA
+            gateup_core<(NT < 8 ? NT : 8), Q8OK, (MFOK && NT >= 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+        else
+            gateup_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);
+    } else {
+        gateup_core<NT, Q8OK, (MFOK && NT > 8)>(s, a, sl, tile, kpi, e, ntok, tok, pair0, stamp);  // > 8 tokens
+    }
 }
 
 // Unit: down tile.  Slot s, 64 output rows over K = F; y written unweighted to ypart[t][q][h] with q = s for a shared
@@ -885,7 +1096,7 @@ __device__ __forceinline__ bool combine_in_unit(const ExpertArgs& a) {
     return a.T * 64 * (a.d.n_shared + a.d.k) <= kCombW * kThreads;
 }
 
-template <int N, bool Q8OK>
+template <int N, bool Q8OK, bool MF = false>
 __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank, DownStamps& st, bool comb, const lds_RouteTab* crt) {
     const int H = a.d.H, F = a.d.F;
@@ -894,19 +1105,24 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     // the weight stream starts first: its first bank is in flight while the act rows are polled (a second bank
     // here, or the act loads ahead of the bank, measured slower)
     const bool q8 = Q8OK && a.int8 && e >= 0;  // Q8OK false: no int8 code in this instantiation
-    TileStream<N, false, MOE_DN_DEPTH> tb;
-    TileStream<N, true, MOE_DN_DEPTH> tq;
+    // (MF: the MFMA streams; otherwise the dot2 streams)
+    TileStream<MF ? 1 : N, false, MF ? 1 : MOE_DN_DEPTH> tb;
+    TileStream<MF ? 1 : N, true, MF ? 1 : MOE_DN_DEPTH> tq;
+    MfmaStream<false> mb;
+    MfmaStream<true> mq;
     if (!q8) {
         const uint16_t* base =
             e >= 0 ? a.L.dn + (size_t)e * a.d.dn_stride() : a.L.sdn + (size_t)(-1 - e) * a.d.dn_stride();
         const u32x4* t = reinterpret_cast<const u32x4*>(base) + (size_t)ht * nc * 64;
         const int cpw = nc / kWaves;
-        tb.begin(t, wave * cpw, (wave + 1) * cpw);
+        if constexpr (MF) mb.begin(t, wave * cpw, (wave + 1) * cpw);
+        else tb.begin(t, wave * cpw, (wave + 1) * cpw);
     } else {
         const int ncq = F / 16;
         const u32x4* t = reinterpret_cast<const u32x4*>(a.L.dn_q8 + (size_t)e * a.d.dn_stride()) + (size_t)ht * ncq * 64;
         const int cpw = ncq / kWaves;
-        tq.begin(t, wave * cpw, (wave + 1) * cpw);
+        if constexpr (MF) mq.begin(t, wave * cpw, (wave + 1) * cpw);
+        else tq.begin(t, wave * cpw, (wave + 1) * cpw);
     }
     // the slot's act rows, published by the gate|up tiles' last parts: 8 loads per thread in flight, then polled
     const uint64_t* src = a.act + (size_t)sl * a.d.max_t * (F / 2);
@@ -932,8 +1148,15 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     float acc[N];
 #pragma unroll
     for (int j = 0; j < N; j++) acc[j] = 0.f;
-    if (!q8) tb.run(s.as, xoff, acc);
-    else tq.run(s.as, xoff, acc);
+    f32x4_t d[4] = {};
+    if constexpr (MF) {
+        const int xo = mfma_xoff<N>(xoff, ntok);
+        if (!q8) mb.run(s.as, xo, d);
+        else mq.run(s.as, xo, d);
+    } else {
+        if (!q8) tb.run(s.as, xoff, acc);
+        else tq.run(s.as, xoff, acc);
+    }
     if (st.on) st.run = __builtin_amdgcn_s_memrealtime();
     const int S = a.d.n_shared, k = a.d.k, kq = S + k, ne = a.T * 64;
     // combiner (comb; crt is its routing table): word w = q * ne + t * 64 + row of the tile; this unit's own terms
@@ -962,7 +1185,8 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
         for (int m = 0; m < kCombW; m++)
             if (cneed(m)) cw[m] = ld_sync(cptr(m));
     }
-    reduce_waves<N>(s.red, acc, N);
+    if constexpr (MF) reduce_waves_mfma<N>(s.red, d, ntok);
+    else reduce_waves<N>(s.red, acc, N);
     const float scale = q8 ? a.L.sc_q8[(size_t)e * (2 * F + H) + 2 * F + ht * 64 + lane] : 1.f;
     if (wave == 0 && !comb) {  // a combiner's own outputs are read by no other unit
         const int h = ht * 64 + lane;
@@ -1017,14 +1241,20 @@ __device__ __forceinline__ void down_core(const Lds& s, const ExpertArgs& a, int
     __syncthreads();  // s.as / s.red are reused by the next unit
 }
 
-template <int NT, bool Q8OK = true>
+template <int NT, bool Q8OK = true, bool MFOK = false>
 __device__ __forceinline__ void down_unit(const Lds& s, const ExpertArgs& a, int sl, int ht, int e, int ntok, const int* tok,
                           const int* rank, DownStamps& st, bool comb = false, const lds_RouteTab* crt = nullptr) {
     if (ntok <= 1 || NT == 1) down_core<1, Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
     else if (ntok <= 2 || NT == 2) down_core<(NT < 2 ? NT : 2), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
     else if (ntok <= 4 || NT == 4) down_core<(NT < 4 ? NT : 4), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else if (ntok <= 8 || NT == 8) down_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
-    else down_core<NT, Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    else if (ntok <= 8 || NT == 8) {
+        if (MFOK && NT >= 8 && a.T >= 8)  // the batch >= 8 grouped case: MFMA
+            down_core<(NT < 8 ? NT : 8), Q8OK, (MFOK && NT >= 8)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+        else
+            down_core<(NT < 8 ? NT : 8), Q8OK>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);
+    } else {
+        down_core<NT, Q8OK, (MFOK && NT > 8)>(s, a, sl, ht, e, ntok, tok, rank, st, comb, crt);  // > 8 tokens
+    }
 }
 
 // Combine 64-row output tile ht of every token from the routing table rt: (out or 0) + shared terms in order + gate *
@@ -1109,13 +1339,10 @@ __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T,
                                                      unsigned epoch) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     const Lds s = lds_carve(lds_raw, T, 1, d.H, d.F, d.E);
-    const int e0 = blockIdx.x * kRouterRows;
+    const int e0 = blockIdx.x * kRouterRows, t0 = blockIdx.y * kRouterTG;
     uint64_t u0 = 0, u1 = 0;  // stamps (unused)
     if (T <= 1) router_unit<1>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
-    else if (T <= 2) router_unit<2>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
-    else if (T <= 4) router_unit<4>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
-    else if (T <= 8) router_unit<8>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
-    else router_unit<kMaxTokens>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1);
+    else router_unit<kRouterTG>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1, t0);
 }
 
 __global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
@@ -1146,7 +1373,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     v.load(a.slots, sl);
     stage_in(s, a.in, a.T, a.d.H);
     uint64_t stamp = 0;
-    gateup_unit<NT>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, stamp);
+    gateup_unit<NT, true, true>(s, a, sl, tile, kpi, v.expert, v.ntok, v.tok, v.pair0, stamp);
 }
 
 // Routing table of the combine, from the published slot table.
@@ -1170,7 +1397,7 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
         SlotView<NT> v;
         v.load(a.slots, sl);
         DownStamps stamp;
-        down_unit<NT>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, stamp);
+        down_unit<NT, true, true>(s, a, sl, ht, v.expert, v.ntok, v.tok, v.rank, stamp);
     }
     if (sl == a.maxs - 1) {  // the last slot's unit of each tile combines it
         load_combine_table(rt, a.slots, a.T, a.d.k);
@@ -1235,6 +1462,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
     Sync* sy = f.sync;
     const int H = a.d.H, F = a.d.F, S = a.d.n_shared;
+    const int nRG = (a.d.E + kRouterRows - 1) / kRouterRows;  // router row groups (router unit u: u % nRG, u / nRG)
     const int ntile = F / 32, nht = H / 64, g = ntile * a.kp, gs = ntile * a.kps;
     const int maxs = a.maxs;
     // The list is laid out for maxs slots; with 2 to 8 tokens, once the routing is known every workgroup trims
@@ -1261,18 +1489,23 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
     };
     auto ensure_routed = [&]() __attribute__((always_inline)) {
         if (!s_routed) {
-            if (route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
+            if (route_local<(NT > 1)>(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
                             a.d.E, a.d.k, a.keep, S, f.do_topk, f.rule, f.do_topk ? f.router_poll : -1)) {
                 // Router logits still missing after the bounded wait: a router unit's workgroup is not running (the
                 // grid is not all resident).  Compute every router row here (the same bits: rewriting a logit that
                 // its unit also writes is harmless), then wait for them without a limit.
                 ensure_staged();
                 uint64_t u0 = 0, u1 = 0;  // stamps (unused)
-                for (int r = 0; r < f.nR; r++)
-                    router_unit<NT>(s, a.L.wr, r * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, false, a.in,
-                                    false, u0, u1);
+                for (int r = 0; r < f.nR; r++) {
+                    if (NT == 1)
+                        router_unit<1>(s, a.L.wr, r * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, false,
+                                       a.in, false, u0, u1);
+                    else
+                        router_unit<kRouterTG>(s, a.L.wr, (r % nRG) * kRouterRows, a.d.E, H, a.T, f.logits, nullptr,
+                                               a.epoch, false, a.in, false, u0, u1, (r / nRG) * kRouterTG);
+                }
                 __syncthreads();
-                route_local(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
+                route_local<(NT > 1)>(rt, (LDS_AS unsigned char*)s.as, f.logits, a.epoch, a.err, a.L.bias, a.ids, a.gates, a.T,
                             a.d.E, a.d.k, a.keep, S, f.do_topk, f.rule, -1);
             }
             if (threadIdx.x == 0) s_routed = 1;
@@ -1309,8 +1542,13 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedArgs f) {
         uint64_t& aux = t_aux;
         if (ur.kind == 0) {
             const bool stage = !s_staged;
-            router_unit<NT>(s, a.L.wr, ur.idx * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, stage, a.in,
-                            f.trace != nullptr, t_aux, t_aux2);
+            if (NT == 1)
+                router_unit<1>(s, a.L.wr, ur.idx * kRouterRows, a.d.E, H, a.T, f.logits, nullptr, a.epoch, stage, a.in,
+                               f.trace != nullptr, t_aux, t_aux2);
+            else
+                router_unit<kRouterTG>(s, a.L.wr, (ur.idx % nRG) * kRouterRows, a.d.E, H, a.T, f.logits, nullptr,
+                                       a.epoch, stage, a.in, f.trace != nullptr, t_aux, t_aux2,
+                                       (ur.idx / nRG) * kRouterTG);
             if (stage && threadIdx.x == 0) s_staged = 1;
         } else if (ur.kind == 1) {
             ensure_routed();
@@ -1575,8 +1813,8 @@ hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const StageSr
     const size_t lds = lds_bytes(T, 1, d.H, d.F, d.E);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&router_kernel), lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(router_kernel, dim3(nblk(d.E, kRouterRows)), dim3(256), lds, st, L, d, T, in, logits, logits_out,
-                       epoch);
+    const dim3 grid(nblk(d.E, kRouterRows), T > 1 ? nblk(T, kRouterTG) : 1);  // (row groups, token groups)
+    hipLaunchKernelGGL(router_kernel, grid, dim3(256), lds, st, L, d, T, in, logits, logits_out, epoch);
     return hipGetLastError();
 }
 
