@@ -242,6 +242,17 @@ def bench_attn(args) -> None:
     ev_us = e0.elapsed_time(e1) / K * 1e3
     nbytes = 2 * S * NKV * D * 2
     achieved = nbytes / (ev_us * 1e-6) / 1e9
+    if args.copy_calibration > 0:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {args.copy_calibration} MiB")
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -267,7 +278,8 @@ def bench_attn(args) -> None:
                    "n_q_heads": NQ, "n_kv_heads": NKV, "head_dim": D, "kv_len": S, "tokens": 1},
         "roofline": {"kernel": "attn_fused_kernel", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes_per_launch": nbytes, "avg_us": round(ev_us, 2),
+                     "traffic": measured_traffic("attn_fused_kernel", "attn"), "bytes_per_launch": nbytes,
+                     "avg_us": round(ev_us, 2),
                      "timing": "timed-region hipEvents on the call's stream (one kernel per call)"},
         "cpu_baseline": cpu,
     }
@@ -476,7 +488,7 @@ def bench_decode(args) -> None:
         "config": {"workload": "decode: 48 layers x (RMSNorm + GQA attention 32q/8kv d128 over KV 4096 + RMSNorm + "
                                "Solar MoE block H4096 F1280 E128+1 top-8) + LM head V196608, greedy, batch 1",
                    "layers": L, "kv_len": DEC_CTX, "vocab": V, "tokens": 1},
-        "roofline": {"kernel": "whole step (7 launches per layer + head)", "bound": "hbm", "achieved": round(achieved, 1),
+        "roofline": {"kernel": "whole step (5 launches per layer + head)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                      "bytes_per_launch": int(nbytes), "avg_us": round(ev_s / K * 1e6, 1),
                      "timing": "timed-region hipEvents on the model's stream over K chained steps"},
