@@ -253,6 +253,13 @@ int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row
  * [max_ctx, NKV, D]).  Device pointers, enqueued on `stream`. */
 int moe_rope_append_dev(int n_q_heads, int n_kv_heads, int head_dim, uint16_t* qkv, const uint16_t* cos_row,
                         const uint16_t* sin_row, uint16_t* k_cache, uint16_t* v_cache, int pos, void* stream);
+/* The q|k|v projection and the step above in one launch (main.rs:109-118: rmsnorm when norm_w, gemv(q|k|v_proj),
+ * round_bf, rope(q), rope(k), the cache append): W [(NQ + 2 NKV) * 128, H] bf16 (the q, k and v tables stacked), x [H]
+ * bf16; q [NQ * 128] receives roped q, k_cache / v_cache row pos the roped k and the v.  head_dim 128, H % 4096 == 0.
+ * Bit-identical to moe_gemv_norm_dev (or moe_gemv_dev) followed by moe_rope_append_dev. */
+int moe_qkv_rope_append_dev(int H, int n_q_heads, int n_kv_heads, int head_dim, const uint16_t* W, const uint16_t* x,
+                            const uint16_t* norm_w, float eps, const uint16_t* cos_row, const uint16_t* sin_row,
+                            uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, int pos, void* stream);
 
 /* ----------------------------------------------------------------------------------------------- decode attention
  * GQA attention of one token over a layer's KV cache, replacing the host step's core (track2_opt/solar_engine/src/

@@ -2,9 +2,9 @@
 //
 // Replaces the reference engine's host step (track2_opt/solar_engine/src/main.rs:372-387 `step`, with `layer`
 // :106-126 and `moe_host` :128-141 per layer): the embedding row of the token, then per layer
-//   h  = rmsnorm(x, input_layernorm)                       folded into the q|k|v GEMV (moe_gemv_norm_dev)
-//   q, k, v = round_bf(gemv(q|k|v_proj, h))                one [QD + 2 KVD, H] table, one launch
-//   rope(q), rope(k), kc[pos] = k, vc[pos] = v             one launch (moe_rope_append_dev)
+//   h  = rmsnorm(x, input_layernorm)                       folded into the q|k|v GEMV (moe_qkv_rope_append_dev)
+//   q, k, v = round_bf(gemv(q|k|v_proj, h))                one [QD + 2 KVD, H] table, one launch, whose epilogue
+//   rope(q), rope(k), kc[pos] = k, vc[pos] = v             ropes q and k and appends k and v to the caches
 //   a  = attention(q, kc[0..pos], vc[0..pos])              moe_attn_decode_dev
 //   o  = round_bf(gemv(o_proj, a))                         moe_gemv_dev
 //   x  = bf16(x + o); h2 = rmsnorm(x, post_attention_layernorm); x = bf16(x + bf16(bf16(moe) + bf16(shared)))
@@ -137,11 +137,9 @@ int run_step(moe_model* m, const int32_t* token, int pos, int32_t* next, float* 
     const float scale = 1.0f / sqrtf((float)c.head_dim);
     uint16_t *x = m->x, *xn = m->x2;
     for (int l = 0; l < m->active_layers; l++) {
-        SUB(m, moe_gemv_norm_dev(m->QD + 2 * m->KVD, c.H, m->qkv_w[l], x, m->in_norm[l], c.eps, m->qkv, m->stream),
-            "q|k|v projection");
-        SUB(m, moe_rope_append_dev(c.n_q_heads, c.n_kv_heads, c.head_dim, m->qkv, cs, sn, m->kc[l], m->vc[l], pos,
-                                   m->stream),
-            "rope / kv append");
+        SUB(m, moe_qkv_rope_append_dev(c.H, c.n_q_heads, c.n_kv_heads, c.head_dim, m->qkv_w[l], x, m->in_norm[l], c.eps,
+                                       cs, sn, m->qkv, m->kc[l], m->vc[l], pos, m->stream),
+            "q|k|v projection, rope, kv append");
         SUB(m, moe_attn_decode_dev(c.n_q_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->qkv, m->kc[l], m->vc[l],
                                    m->attn, m->attn_ws, m->attn_ws_bytes, m->stream),
             "attention");

@@ -32,10 +32,30 @@ __device__ __forceinline__ float wave_sum(float v) {
 // 16-byte chunks of x and of the weight loaded at once; the squares summed per thread over its chunks in order, then a
 // 64-lane butterfly, then the 4 wavefronts in order): the layer's input norm folded into its q|k|v projection.
 constexpr int kXC = 4;  // 16-byte chunks of x per thread per staging pass (one pass for K <= 8192)
-template <int RB, int CG>
+
+// ROPE (the q|k|v projection with RoPE and the KV append in its epilogue, main.rs:109-118): y = qkv rows of 128-wide
+// heads [q (NQ) | k (NKV) | v (NKV)]; wave step s takes rows (h = s / 32, p = s % 32) 128 h + 2p, + 1, + 64, + 65, i.e.
+// two element pairs that RoPE rotates into each other, so the step's four sums give four roped outputs: q heads go to
+// y, k heads to the key cache row of pos, v heads (not rotated) to the value cache row.  The sums, the roundings and
+// RoPE's arithmetic are those of the plain GEMV followed by rope_append_kernel, so the bits are the same.
+struct RopeArgs {
+    const uint16_t* cs;  // cos row of pos [128]
+    const uint16_t* sn;  // sin row of pos [128]
+    uint16_t* kc;        // key cache row of pos [NKV, 128]
+    uint16_t* vc;        // value cache row of pos [NKV, 128]
+    int NQ, NKV;
+};
+template <bool ROPE, int RB>
+__device__ __forceinline__ int step_row(int s, int r) {  // row r of wave step s
+    if (!ROPE) return s * RB + r;
+    return (s >> 5) * 128 + 2 * (s & 31) + (r & 1) + ((r >> 1) << 6);
+}
+
+template <int RB, int CG, bool ROPE = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ y, int M, int K,
-                                                   const uint16_t* __restrict__ norm_w, float eps) {
+                                                   const uint16_t* __restrict__ norm_w, float eps, RopeArgs ra) {
+    static_assert(!ROPE || RB == 4, "RoPE steps take 4 rows");
     extern __shared__ __align__(16) uint16_t xs[];
     __shared__ float red[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -45,17 +65,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) acc[r] = 0.f;
-    auto load_group = [&](int r0_, int c0_) {
+    const int nsteps = (M + RB - 1) / RB;
+    auto load_group = [&](int s_, int c0_) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int row = r0_ + r < M ? r0_ + r : M - 1;  // rows past M re-read the last row; discarded below
+            int row = step_row<ROPE, RB>(s_, r);
+            row = row < M ? row : M - 1;  // rows past M re-read the last row; discarded below
             const u32x4* wr = reinterpret_cast<const u32x4*>(W + (size_t)row * K);
 #pragma unroll
             for (int c = 0; c < CG; ++c) wq[r][c] = __builtin_nontemporal_load(&wr[(c0_ + c) * 64 + lane]);
         }
     };
-    int r0 = gw * RB, c0 = 0;
-    if (r0 < M) load_group(r0, 0);
+    int st = gw, c0 = 0;  // wave step, chunk group
+    if (st < nsteps) load_group(st, 0);
     // stage x (normalised when norm_w): thread tid holds 16-byte chunks tid + 256 j
     const int nc = K / 8;
     const u32x4* x4 = reinterpret_cast<const u32x4*>(x);
@@ -118,7 +140,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
         }
     }
     __syncthreads();
-    while (r0 < M) {
+    while (st < nsteps) {
 #pragma unroll
         for (int c = 0; c < CG; ++c) {
             const u32x4 h4 = *reinterpret_cast<const u32x4*>(&xs[((c0 + c) * 64 + lane) * 8]);
@@ -135,21 +157,47 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
                 acc[r] = s;
             }
         }
-        int nr0 = r0, nc0 = c0 + CG;
+        int nst = st, nc0 = c0 + CG;
         if (nc0 >= nch) {
             nc0 = 0;
-            nr0 = r0 + nw * RB;
+            nst = st + nw;
         }
-        if (nr0 < M) load_group(nr0, nc0);
+        if (nst < nsteps) load_group(nst, nc0);
         if (nc0 == 0) {
+            if constexpr (!ROPE) {
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                const float tot = wave_sum(acc[r]);
-                acc[r] = 0.f;
-                if (lane == r && r0 + r < M) y[r0 + r] = (uint16_t)f2bf(tot);
+                for (int r = 0; r < RB; ++r) {
+                    const float tot = wave_sum(acc[r]);
+                    acc[r] = 0.f;
+                    if (lane == r && st * RB + r < M) y[st * RB + r] = (uint16_t)f2bf(tot);
+                }
+            } else {
+                float xb[4];  // the four rows' bf16 results: rows i, i + 1 (first half) and i + 64, i + 65
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    xb[r] = bf2f(f2bf(wave_sum(acc[r])));
+                    acc[r] = 0.f;
+                }
+                const int h = st >> 5, i = 2 * (st & 31);
+                if (lane < 4) {
+                    const int r = lane, e = i + (r & 1) + ((r >> 1) << 6);  // this lane's element of the head
+                    const float own = xb[r];
+                    uint16_t out;
+                    if (h < ra.NQ + ra.NKV) {  // q or k: rot = -x[e + 64] for e < 64, x[e - 64] above
+                        const float rot = r < 2 ? -xb[r + 2] : xb[r - 2];
+                        const float av = bf2f(f2bf(own * bf2f(ra.cs[e])));
+                        const float bv = bf2f(f2bf(rot * bf2f(ra.sn[e])));
+                        out = (uint16_t)f2bf(av + bv);
+                    } else {
+                        out = (uint16_t)f2bf(own);
+                    }
+                    if (h < ra.NQ) y[(size_t)h * 128 + e] = out;
+                    else if (h < ra.NQ + ra.NKV) ra.kc[(size_t)(h - ra.NQ) * 128 + e] = out;
+                    else ra.vc[(size_t)(h - ra.NQ - ra.NKV) * 128 + e] = out;
+                }
             }
         }
-        r0 = nr0;
+        st = nst;
         c0 = nc0;
     }
 }
@@ -252,14 +300,14 @@ int gemv_grid(const void* fn, size_t lds, int M, int RB, int* grid) {
     return MOE_GPU_OK;
 }
 
-template <int RB, int CG>
+template <int RB, int CG, bool ROPE = false>
 int gemv_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, int M, int K, const uint16_t* norm_w, float eps,
-                hipStream_t st) {
-    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<RB, CG>);
+                hipStream_t st, RopeArgs ra = RopeArgs{}) {
+    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<RB, CG, ROPE>);
     const size_t lds = (size_t)K * sizeof(uint16_t);
     int grid = 0, rc = gemv_grid(fn, lds, M, RB, &grid);
     if (rc != MOE_GPU_OK) return rc;
-    hipLaunchKernelGGL((gemv_kernel<RB, CG>), dim3(grid), dim3(256), lds, st, W, x, y, M, K, norm_w, eps);
+    hipLaunchKernelGGL((gemv_kernel<RB, CG, ROPE>), dim3(grid), dim3(256), lds, st, W, x, y, M, K, norm_w, eps, ra);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_GPU_OK : e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
 }
@@ -312,6 +360,19 @@ int moe_rope_append_dev(int n_q_heads, int n_kv_heads, int head_dim, uint16_t* q
                        n_kv_heads, head_dim, pos);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_GPU_OK : e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP;
+}
+
+int moe_qkv_rope_append_dev(int H, int n_q_heads, int n_kv_heads, int head_dim, const uint16_t* W, const uint16_t* x,
+                            const uint16_t* norm_w, float eps, const uint16_t* cos_row, const uint16_t* sin_row,
+                            uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, int pos, void* stream) {
+    if (H < 4096 || H % 4096 != 0 || H > 65536 || n_q_heads < 1 || n_kv_heads < 1 || head_dim != 128 || pos < 0 ||
+        !W || !x || !cos_row || !sin_row || !q || !k_cache || !v_cache || (norm_w && !(eps >= 0.f)))
+        return MOE_GPU_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15) return MOE_GPU_EINVAL;
+    const size_t row = (size_t)pos * n_kv_heads * 128;
+    const RopeArgs ra{cos_row, sin_row, k_cache + row, v_cache + row, n_q_heads, n_kv_heads};
+    return gemv_launch<4, 8, true>(W, x, q, (n_q_heads + 2 * n_kv_heads) * 128, H, norm_w, eps,
+                                   static_cast<hipStream_t>(stream), ra);
 }
 
 int moe_rope_dev(int n_heads, int head_dim, uint16_t* x, const uint16_t* cos_row, const uint16_t* sin_row,

@@ -39,6 +39,7 @@ SYMBOLS = (
     "moe_head_create", "moe_head_destroy", "moe_head_last_error", "moe_head_set_stream", "moe_head_synchronize",
     "moe_head_load", "moe_head_load_dev", "moe_head_argmax", "moe_head_argmax_dev",
     "moe_rmsnorm_dev", "moe_gemv_dev", "moe_gemv_f32_dev", "moe_gemv_norm_dev", "moe_rope_dev", "moe_rope_append_dev",
+    "moe_qkv_rope_append_dev",
     "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error", "moe_attn_noalloc_max_bytes",
     "moe_attn_decode_noalloc_dev",
     "moe_gpu_block_dev",
@@ -150,6 +151,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_gemv_norm_dev": (i, [i, i, vp, vp, vp, f, vp, vp]),
         "moe_gemv_f32_dev": (i, [i, i, vp, vp, vp, vp]),
         "moe_rope_append_dev": (i, [i, i, i, vp, vp, vp, vp, vp, i, vp]),
+        "moe_qkv_rope_append_dev": (i, [i, i, i, i, vp, vp, vp, f, vp, vp, vp, vp, vp, i, vp]),
         "moe_gpu_block_dev": (i, [vp, i, i, vp, vp, vp, f, i, u, vp, vp, vp, vp]),
         "moe_model_create": (i, [i, C.POINTER(ModelConfig), C.POINTER(vp)]),
         "moe_model_destroy": (None, [vp]),
@@ -544,6 +546,19 @@ def rope_append_dev(qkv, cos_row, sin_row, k_cache, v_cache, pos: int, n_q_heads
                                             _p(k_cache), _p(v_cache), pos, getattr(stream, "cuda_stream", stream))
     if rc != OK:
         raise MoeGpuError(rc, "moe_rope_append_dev failed")
+
+
+def qkv_rope_append_dev(W, x, norm_w, cos_row, sin_row, q, k_cache, v_cache, pos: int, n_q_heads: int,
+                        n_kv_heads: int, eps: float = 1e-5, stream=None) -> None:
+    """The q|k|v projection (rmsnorm folded in when norm_w is given), RoPE and the KV-cache append in one launch:
+    q [NQ * 128] receives roped q, the caches' row pos the roped k and the v (main.rs:109-118)."""
+    M, K = W.shape
+    rc = load_library().moe_qkv_rope_append_dev(K, n_q_heads, n_kv_heads, 128, _p(W), _p(x),
+                                                _p(norm_w) if norm_w is not None else None, eps, _p(cos_row),
+                                                _p(sin_row), _p(q), _p(k_cache), _p(v_cache), pos,
+                                                getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, f"moe_qkv_rope_append_dev(H={K}, NQ={n_q_heads}, NKV={n_kv_heads}) failed")
 
 
 class MoeModel:

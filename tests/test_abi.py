@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "moe_gpu.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(moe_(?:gpu|head|attn|rmsnorm|gemv|rope|model|st|placement)_?\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(moe_(?:gpu|head|attn|rmsnorm|gemv|rope|qkv|model|st|placement)_?\w+)\s*\(", text)))
 
 
 def test_header_declares_the_wrapped_symbols():
@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(L, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", moe_gpu.LIB_PATH], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\bT (moe_(?:gpu|head|attn|rmsnorm|gemv|rope|model|st|placement)_?\w+)", out))
+    exported = set(re.findall(r"\bT (moe_(?:gpu|head|attn|rmsnorm|gemv|rope|qkv|model|st|placement)_?\w+)", out))
     assert set(declared_functions()) <= exported
 
 

@@ -133,6 +133,44 @@ def test_rope_append_bitexact():
     np.testing.assert_array_equal(host(vd).reshape(CTX, NKV, D), vc2)
 
 
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_qkv_rope_append_equals_the_two_launches(with_norm):
+    """moe_qkv_rope_append_dev (the q|k|v GEMV with RoPE and the cache append in its epilogue) gives the bits of
+    moe_gemv_norm_dev / moe_gemv_dev followed by moe_rope_append_dev; no other cache row changes."""
+    import torch
+
+    from moe_gpu import gemv_dev, gemv_norm_dev, qkv_rope_append_dev, rope_append_dev
+
+    NQ, NKV, D, H, CTX, pos = 32, 8, 128, 4096, 16, 11
+    M = (NQ + 2 * NKV) * D
+    rng = np.random.default_rng(77)
+    W = dev(O.f2bf((0.02 * rng.standard_normal((M, H))).astype(np.float32))).view(M, H)
+    x = dev(O.f2bf(rng.standard_normal(H).astype(np.float32)))
+    nw = dev(O.f2bf(rng.uniform(0.5, 1.5, H).astype(np.float32))) if with_norm else None
+    th = rng.uniform(0, 200, D // 2)
+    c = dev(O.f2bf(np.cos(np.concatenate([th, th])).astype(np.float32)))
+    s = dev(O.f2bf(np.sin(np.concatenate([th, th])).astype(np.float32)))
+    kc0 = O.f2bf(rng.standard_normal((CTX, NKV, D)).astype(np.float32))
+    vc0 = O.f2bf(rng.standard_normal((CTX, NKV, D)).astype(np.float32))
+    k1, v1, k2, v2 = dev(kc0), dev(vc0), dev(kc0), dev(vc0)
+    qkv = torch.zeros(M, dtype=torch.int16, device="cuda:0")
+    q2 = torch.zeros(NQ * D, dtype=torch.int16, device="cuda:0")
+    say(f"qkv + rope + append, norm={with_norm}")
+    torch.cuda.synchronize()
+    if with_norm:
+        gemv_norm_dev(W, x, nw, qkv)
+    else:
+        gemv_dev(W, x, qkv)
+    rope_append_dev(qkv, c, s, k1, v1, pos, NQ, NKV)
+    qkv_rope_append_dev(W, x, nw, c, s, q2, k2, v2, pos, NQ, NKV)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(q2), host(qkv)[:NQ * D])
+    np.testing.assert_array_equal(host(k2), host(k1))
+    np.testing.assert_array_equal(host(v2), host(v1))
+    kd = host(k2).reshape(CTX, NKV, D)
+    np.testing.assert_array_equal(np.delete(kd, pos, axis=0), np.delete(kc0, pos, axis=0))
+
+
 def test_gemv_f32_bit_identical_to_ck_gemv():
     """moe_gemv_f32_dev runs ck_gemv's own summation order (two 16-lane vdpbf16ps accumulators, GCC's reduce tree)."""
     import torch
