@@ -93,6 +93,64 @@ def cpu_baseline(w: Workload, budget_s: float = 12.0) -> dict | None:
                       f"{ne}-expert pool + router GEMV/top-k), median; {'cpu_kern.c ck_gemv+ck_moe3' if kind == 'reference' else 'scalar restatement'}"}
 
 
+def cpu_baseline_batched(w: Workload, budget_s: float = 12.0) -> dict | None:
+    """The reference's batched CPU path for T > 1 tokens timed on this host: per token ck_gemv router (the reference's
+    own cpu_kern.c build) + host route, the tokens grouped by expert in first-seen order (runtime.py:344-347), then
+    cpu_moe (solar_hybrid/cpu_moe.cpp:38-96) over the shared expert and the grouped routed experts, each weight row
+    streamed once per call for all its tokens.  cpu_moe runs as the oracle's AVX-512 BF16 + OpenMP port of
+    cpu_moe.cpp (its torch-extension build is not made here).  Needs an AVX-512 BF16 host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    if not O.ref_available():
+        return None
+    H, F, E, k, T = w.H, w.F, w.E, w.k, w.T
+    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    R = O.Ref()
+    R.set_threads(cores)
+    ne = 48  # distinct expert weight sets rotated beyond the LLC (about 1.5 GB)
+    rng = np.random.default_rng(0)
+    base = O.f2bf((rng.normal(0, 0.02, 3 * F * H)).astype(np.float32))
+    pool = []
+    for i in range(ne):
+        b = np.roll(base, i * 4099)
+        pool.append((np.ascontiguousarray(b[:2 * F * H].reshape(2 * F, H)),
+                     np.ascontiguousarray(b[2 * F * H:].reshape(H, F))))
+    wr = O.f2bf(rng.normal(0, 0.02, (E, H)).astype(np.float32))
+    bias = zipf_bias(E, w.zipf_s, 0)
+    keep = w.keep_eff
+    ts, distinct = [], []
+    t_end = time.perf_counter() + budget_s
+    it = 0
+    while (it < 12 or time.perf_counter() < t_end) and it < 400:
+        x = O.f2bf(rng.normal(0, 1, (T, H)).astype(np.float32))
+        t0 = time.perf_counter()
+        lg = np.stack([R.gemv(wr, x[t]) for t in range(T)])
+        ids, gates = O.route(lg, bias, k, keep)
+        groups = O.group_tokens(ids, gates, keep)
+        gus, ds, toks, ws = [], [], [], []
+        for s in range(w.n_shared):  # the shared expert: every token, weight 1
+            g, d = pool[(it * 37 + s) % ne]
+            gus.append(g); ds.append(d); toks.append(np.arange(T, dtype=np.int64)); ws.append(np.ones(T, np.float32))
+        for j, (e, tk, wt) in enumerate(groups):
+            g, d = pool[(it * 37 + w.n_shared + j) % ne]
+            gus.append(g); ds.append(d); toks.append(tk); ws.append(wt)
+        O.cpu_moe_port(x, gus, ds, toks, ws)
+        dt = time.perf_counter() - t0
+        if it >= 2:
+            ts.append(dt)
+            distinct.append(len(groups))
+        it += 1
+    med = statistics.median(ts)
+    nbytes = w.router_bytes() + (float(np.mean(distinct)) + w.n_shared) * 3 * F * H * 2
+    return {"value": round(med * 1e6 / T, 1), "unit": "us/layer/token", "cores": cores, "kind": "port",
+            "GBps": round(nbytes / med / 1e9, 1), "us_per_call": round(med * 1e6, 1),
+            "sample": f"{len(ts)} calls of {T} tokens: ck_gemv router per token (cpu_kern.c build) + host route + "
+                      f"first-seen grouping + cpu_moe (cpu_moe.cpp:38-96, the oracle's AVX-512 BF16/OpenMP port) over "
+                      f"the shared expert and {np.mean(distinct):.1f} distinct routed experts from a {ne}-set pool, "
+                      f"median"}
+
+
 LM_HEAD_H, LM_HEAD_V = 4096, 196608
 LM_HEAD_METRIC = "LM head (final RMSNorm + GEMV over V=196608 + greedy argmax) µs/token + achieved HBM TB/s, bf16 batch 1"
 
@@ -659,9 +717,9 @@ def main():
         del src, dst
 
     cpu = None
-    if not args.no_cpu_baseline and w.T == 1:
+    if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu = cpu_baseline(w)
+        cpu = cpu_baseline(w) if w.T == 1 else cpu_baseline_batched(w)
 
     us_tok = ms_per_step * 1e3 / T
     line = {

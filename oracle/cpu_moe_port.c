@@ -1,9 +1,9 @@
 /*
  * cpu_moe_port.c — AVX-512 BF16 + OpenMP port of solar_hybrid/cpu_moe.cpp:38-96 (the CPU baseline "port").
  *
- * TEST INFRASTRUCTURE ONLY: checked bit-for-bit against the scalar restatement in moe_oracle.c by the tests (the
- * benchmark's cpu_baseline leg times the reference's own cpu_kern.c build, oracle/_ref, or, where that cannot be loaded,
- * the scalar restatement; it does not time this port).
+ * TEST INFRASTRUCTURE ONLY: checked bit-for-bit against the scalar restatement in moe_oracle.c by the tests.  The
+ * benchmark's cpu_baseline leg times it for the batched workloads (T > 1 tokens, cpu_moe.cpp's own use); batch 1 times
+ * the reference's own cpu_kern.c build (oracle/_ref) or, where that cannot be loaded, the scalar restatement.
  * Built into its own library with AVX-512 flags so that the scalar oracle stays loadable on any x86-64 host.
  */
 #include <math.h>
