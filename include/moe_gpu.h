@@ -271,7 +271,7 @@ int moe_qkv_rope_append_dev(int H, int n_q_heads, int n_kv_heads, int head_dim, 
  * stream), not synchronised; one kernel launch, which may be captured in a HIP graph and replayed.  The caller
  * passes a device workspace of moe_attn_workspace_bytes() bytes (0 for arguments out of range) dedicated to these
  * calls, zero-filled before its first call: a 256-byte header (the call counter), the call's scores ([NQ, S] fp32
- * from byte 256, left there for the caller), then tagged per-chunk statistics and partials.  Between calls nothing
+ * from byte 256, left there for the caller), then tagged per-chunk statistics, partials and outputs.  Between calls nothing
  * else may write it (zeroing all of it again is allowed).  Pass the same workspace_bytes on every call on a
  * workspace.  Calls that share a workspace and overlap in time (two streams) race. */
 size_t moe_attn_workspace_bytes(int n_q_heads, int head_dim, int S);
@@ -279,10 +279,17 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
                         const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace,
                         size_t workspace_bytes, void* stream);
 const char* moe_attn_last_error(void); /* message of this thread's last failed moe_attn_decode_dev */
+/* moe_attn_decode_dev with the layer's o projection folded into the same launch, replacing main.rs:86-104 and :119
+ * (attention, then round_bf(gemv(o_proj, attention output))): out as moe_attn_decode_dev, and o_out [o_rows] bf16 =
+ * bf16(w_o . out) with w_o [o_rows, NQ * D] bf16 row-major (16-byte aligned), bit-identical to moe_gemv_dev(o_rows,
+ * NQ * D, w_o, out, o_out).  Needs NQ * D = 4096; same workspace and rules as moe_attn_decode_dev. */
+int moe_attn_decode_oproj_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                              const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, const uint16_t* w_o,
+                              int o_rows, uint16_t* o_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Allocation-free variant of moe_attn_decode_dev.  No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
- * workspace lives in a file-scope device array of moe_attn_noalloc_max_bytes() bytes (6.3 MB: 64 query heads x 8192
+ * workspace lives in a file-scope device array of moe_attn_noalloc_max_bytes() bytes (6.4 MB: 64 query heads x 8192
  * positions), one per GPU, held until the process ends; its address is looked up once per device.  The call
  * allocates nothing (its first call on a device also enqueues the clearing of the array: make that call outside a
  * graph capture); it returns MOE_GPU_EINVAL, enqueueing nothing, when moe_attn_workspace_bytes(n_q_heads,

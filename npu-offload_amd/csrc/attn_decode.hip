@@ -14,6 +14,7 @@
 #include <stddef.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 
@@ -59,6 +60,9 @@ constexpr int kVP = kP / kWv;    // positions per wave in the P.V product
 constexpr int kMaxC = 512;       // chunks per kv head (S <= 65536)
 
 constexpr unsigned kEpochWrap = 0xFFFF0000u;
+constexpr int kOK = 4096;             // o projection: columns (NQ * kD), one 8-chunk load group per lane per row
+constexpr int kOC = kOK / 512;        // 16-byte chunks per lane per row
+constexpr int kORows = 2 * (kT / 64); // o rows per workgroup: two per wave
 constexpr size_t kHdrBytes = 256;  // workspace header: [0] last epoch, [1] started, [2] done
 
 struct FusedAttn {
@@ -74,6 +78,11 @@ struct FusedAttn {
     int NQ, NKV, S, C, R, W;  // chunks, chunks per workgroup, workgroups per kv head
     int poll;                 // passes of a wait before the fallback
     float scale;
+    // the o projection folded in (moe_attn_decode_oproj_dev; wo null otherwise): o_out = bf16(wo . out), wo [Mo, NQ*kD]
+    const uint16_t* wo;
+    uint16_t* o_out;
+    uint64_t* aout;  // [NQ * kD] tagged attention outputs (bf16 bits), read by every workgroup's o rows
+    int Mo, Wa;      // o rows; attention workgroups (W * NKV, the first Wa of the grid)
 };
 
 __device__ __forceinline__ unsigned next_epoch(unsigned e) {
@@ -106,6 +115,7 @@ struct AttnLds {
     unsigned char missing[kMaxC];
     int nmiss, anymiss;
     unsigned ep;  // the header's last epoch, as thread 0 read it
+    __attribute__((aligned(16))) uint16_t ox[kOK];  // the o projection's input: every attention output (bf16)
 };
 
 // Scores of chunk c into L.sc (positions past S: -inf), and to the workspace when write_ws, from the chunk's K rows in
@@ -276,6 +286,27 @@ __device__ __forceinline__ void chunk_pv(AttnLds<G>& L, const uint32_t (&vv)[kVP
     __syncthreads();
 }
 
+// M and tot per head from every chunk's statistics in L.mt / L.st (wave w: heads w, w + kWv): M = the max over the
+// chunks; tot = sum_c s_c exp(m_c - M), lane l adding chunks l, l + 64, ... in order, then a wave reduction (the same
+// operations in every workgroup of the group).  The caller has synchronised since L.mt / L.st were written; L.M /
+// L.tot are read after a later barrier.
+template <int G>
+__device__ __forceinline__ void group_totals(AttnLds<G>& L, int C) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int h = w; h < G; h += kWv) {
+        float m = -INFINITY;
+        for (int cc = lane; cc < C; cc += 64) m = fmaxf(m, L.mt[h][cc]);
+        m = wave_reduce(m, MaxOp());
+        float tot = 0.f;
+        for (int cc = lane; cc < C; cc += 64) tot = fmaf(L.st[h][cc], expf(L.mt[h][cc] - m), tot);
+        tot = wave_reduce(tot, AddOp());
+        if (lane == 0) {
+            L.M[h] = m;
+            L.tot[h] = tot;
+        }
+    }
+}
+
 // Tagged words polled in groups of kGW per thread, every load of a group in flight together: the words whose bit is set
 // in `need` are loaded until they carry `epoch`; true when all did within `poll` passes.
 constexpr int kGW = 8;
@@ -299,8 +330,8 @@ __device__ __forceinline__ bool poll_words(uint64_t (&w)[kGW], unsigned need, Pt
 
 // A share whose partials did not all arrive: every chunk's partial is recomputed here in chunk order (the producer's
 // functions) and the whole share summed as the gather does (outputs already written get the same bits).
-template <int G>
-__device__ void share_fallback(const FusedAttn& a, AttnLds<G>& L, int g, int o0, int nout, uint32_t (&vv)[kVP]) {
+template <int G, typename Put>
+__device__ void share_fallback(const FusedAttn& a, AttnLds<G>& L, int g, int o0, int nout, uint32_t (&vv)[kVP], Put put) {
     const int tid = threadIdx.x, C = a.C;
     constexpr int kJ = (G * kD + kT - 1) / kT;
     float sums[kJ];
@@ -326,18 +357,68 @@ __device__ void share_fallback(const FusedAttn& a, AttnLds<G>& L, int g, int o0,
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
         const int i = tid + kT * j;
-        if (i < nout) a.out[(size_t)(g * G + (o0 + i) / kD) * kD + (o0 + i) % kD] = (uint16_t)f2bf(sums[j]);
+        if (i < nout) put((g * G + (o0 + i) / kD) * kD + (o0 + i) % kD, f2bf(sums[j]));
     }
 }
 
-template <int G>
+// Every output of kv head g computed here from the cache (the statistics of every chunk, the totals, every chunk's
+// partial), with the producers' functions, so the bits are theirs: the o projection's fallback for outputs that never
+// arrived.  put(output index, bf16 bits).
+template <int G, typename Put>
+__device__ void group_fallback(const FusedAttn& a, AttnLds<G>& L, int g, uint32_t (&vv)[kVP], Put put) {
+    const int tid = threadIdx.x;
+    for (int cc = 0; cc < a.C; ++cc) {
+        u32x4 kr[kKL];
+        load_k(a, g, cc, kr);
+        store_k<G>(L, kr);
+        chunk_scores<G>(a, L, g, cc, false);
+        chunk_stats<G>(L);
+        if (tid < G) {
+            L.mt[tid][cc] = L.m[tid];
+            L.st[tid][cc] = L.s[tid];
+        }
+        __syncthreads();
+    }
+    group_totals<G>(L, a.C);
+    __syncthreads();
+    share_fallback<G>(a, L, g, 0, G * kD, vv, put);
+}
+
+// Sum over a wave by xor butterflies 32 .. 1 (the order of the dense GEMV's, whose bits the o projection keeps).
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// OPROJ: the o projection folded in.  Workgroup b also owns o rows kORows b .. kORows b + kORows - 1 (wave w: two rows,
+// lane l: 16-byte chunks 64 c + l of each), whose weights it loads once it has published its chunk statistics (so they
+// stream while the exchanges wait); the grid is max(W * NKV, Mo / kORows) workgroups, those past W * NKV only
+// computing o rows.  5. Every attention output arrives as a tagged word (published by step 4); each row is then summed
+// in the dense GEMV's order (lane chunks in order, then a xor butterfly), so o is bit-identical to moe_gemv_dev's.
+template <int G, bool OPROJ>
 __global__ __launch_bounds__(kT) void attn_fused_kernel(FusedAttn a) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     AttnLds<G>& L = *reinterpret_cast<AttnLds<G>*>(lds_raw);
-    const int g = blockIdx.y, wg = blockIdx.x, C = a.C, tid = threadIdx.x;
-    const int c0 = wg * a.R, c1 = min(c0 + a.R, C);  // own chunks
+    const int b = (int)blockIdx.x;
+    const bool attn_wg = !OPROJ || b < a.Wa;
+    const int g = attn_wg ? b / a.W : 0, wg = attn_wg ? b % a.W : 0, C = a.C, tid = threadIdx.x;
+    const int c0 = attn_wg ? wg * a.R : 0, c1 = attn_wg ? min(c0 + a.R, C) : 0;  // own chunks
     const int poll = a.poll;
-    const unsigned long long total = (unsigned long long)gridDim.x * gridDim.y;
+    const unsigned long long total = gridDim.x;
+    const int olane = tid & 63, owv = tid >> 6;
+    const bool has_o = OPROJ && b * kORows < a.Mo;
+    u32x4 wo_r[2][kOC];
+    auto load_wo = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int row = min(b * kORows + 2 * owv + r, a.Mo - 1);  // rows past Mo re-read the last; discarded
+            const u32x4* wr = reinterpret_cast<const u32x4*>(a.wo + (size_t)row * kOK);
+#pragma unroll
+            for (int c = 0; c < kOC; ++c) wo_r[r][c] = __builtin_nontemporal_load(&wr[c * 64 + olane]);
+        }
+    };
+    if (has_o && !attn_wg) load_wo();
     if (tid == 0) {
         L.ep = (unsigned)ld_word(a.hdr);  // read once, by the thread that counts the workgroup as started
         L.anymiss = 0;
@@ -347,6 +428,11 @@ __global__ __launch_bounds__(kT) void attn_fused_kernel(FusedAttn a) {
     unsigned epoch = 0;
     bool wrap = false;
     for (int i = tid; i < C; i += kT) L.missing[i] = 0;
+    if (!attn_wg) {  // (uniform) an o-only workgroup takes the call's epoch here
+        __syncthreads();
+        epoch = next_epoch(L.ep);
+        wrap = epoch >= kEpochWrap;
+    }
     for (int c = c0; c < c1; ++c) {
         u32x4 kr[kKL];
         load_k(a, g, c, kr);
@@ -373,9 +459,16 @@ __global__ __launch_bounds__(kT) void attn_fused_kernel(FusedAttn a) {
             L.st[tid][c] = L.s[tid];
         }
     }
+    if (has_o && attn_wg) load_wo();
     // counted as started (thread 0 read the epoch before); the return is needed only after the waits below
     unsigned long long started = 0;
     if (tid == 0) started = __hip_atomic_fetch_add(a.hdr + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // an attention output: bf16 to `out`, and (OPROJ) a tagged word for every workgroup's o rows
+    auto put_out = [&](int o, uint32_t bits) __attribute__((always_inline)) {
+        a.out[o] = (uint16_t)bits;
+        if (OPROJ) st_word(a.aout + o, ((uint64_t)epoch << 32) | bits);
+    };
+    if (attn_wg) {  // (uniform) steps 2 to 4
     // 2. the other chunks' statistics of the group; item i = (head i / C, chunk i % C), two words each
     for (int i0 = 0; i0 < G * C; i0 += kT * (kGW / 2)) {
         uint64_t w[kGW];
@@ -421,23 +514,7 @@ __global__ __launch_bounds__(kT) void attn_fused_kernel(FusedAttn a) {
             __syncthreads();
         }
     }
-    // M and tot per head (wave w: heads w, w + kWv): M = the max over the chunks; tot = sum_c s_c exp(m_c - M), lane l
-    // adding chunks l, l + 64, ... in order, then a wave reduction (the same operations in every workgroup of the group)
-    {
-        const int lane = tid & 63, w = tid >> 6;
-        for (int h = w; h < G; h += kWv) {
-            float m = -INFINITY;
-            for (int cc = lane; cc < C; cc += 64) m = fmaxf(m, L.mt[h][cc]);
-            m = wave_reduce(m, MaxOp());
-            float tot = 0.f;
-            for (int cc = lane; cc < C; cc += 64) tot = fmaf(L.st[h][cc], expf(L.mt[h][cc] - m), tot);
-            tot = wave_reduce(tot, AddOp());
-            if (lane == 0) {
-                L.M[h] = m;
-                L.tot[h] = tot;
-            }
-        }
-    }
+    group_totals<G>(L, C);
     // 3. p and each own chunk's partial P.V, published (the scores back from the workspace unless L.sc holds them)
     for (int c = c0; c < c1; ++c) {
         if (c != c0) load_v(a, g, c, vv);
@@ -492,11 +569,55 @@ __global__ __launch_bounds__(kT) void attn_fused_kernel(FusedAttn a) {
             }
             for (; cc < C; ++cc) sum = sum + L.tab[cc * n + i];
             const int o = ob + i;
-            a.out[(size_t)(g * G + o / kD) * kD + o % kD] = (uint16_t)f2bf(sum);
+            put_out((g * G + o / kD) * kD + o % kD, f2bf(sum));
         }
         __syncthreads();  // L.tab is refilled by the next pass
     }
-    if (fallback) share_fallback<G>(a, L, g, o0, nout, vv);
+    if (fallback) share_fallback<G>(a, L, g, o0, nout, vv, put_out);
+    }  // steps 2 to 4
+    if (has_o) {  // (uniform) 5. the o rows, from every attention output
+        const int nO = a.NQ * kD;  // == kOK
+        uint64_t w[kGW];
+        unsigned need = 0;
+#pragma unroll
+        for (int j = 0; j < kGW; ++j)
+            if (tid + kT * j < nO) need |= 1u << j;
+        if (tid == 0) L.nmiss = 0;
+        __syncthreads();
+        if (!poll_words(w, need, [&](int j) { return a.aout + tid + kT * j; }, epoch, poll)) L.nmiss = 1;
+#pragma unroll
+        for (int j = 0; j < kGW; ++j)
+            if (need >> j & 1) L.ox[tid + kT * j] = (uint16_t)w[j];
+        __syncthreads();
+        if (L.nmiss) {  // (uniform) an output never arrived (its producer not running): every output computed here
+            for (int gg = 0; gg < a.NKV; ++gg)
+                group_fallback<G>(a, L, gg, vv, [&](int o, uint32_t bits) { L.ox[o] = (uint16_t)bits; });
+            __syncthreads();
+        }
+        float acc[2] = {0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < kOC; ++c) {
+            const u32x4 h4 = *reinterpret_cast<const u32x4*>(&L.ox[(c * 64 + olane) * 8]);
+            const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint32_t ww[4] = {wo_r[r][c].x, wo_r[r][c].y, wo_r[r][c].z, wo_r[r][c].w};
+                float sr = acc[r];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sr = fmaf(__uint_as_float(ww[j] << 16), __uint_as_float(hw[j] << 16), sr);
+                    sr = fmaf(__uint_as_float(ww[j] & 0xFFFF0000u), __uint_as_float(hw[j] & 0xFFFF0000u), sr);
+                }
+                acc[r] = sr;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const float tot = wave_sum_xor(acc[r]);
+            const int row = b * kORows + 2 * owv + r;
+            if (olane == r && row < a.Mo) a.o_out[row] = (uint16_t)f2bf(tot);
+        }
+    }
     // the last workgroup to start stores this call's epoch for the next call (every workgroup has read the header by
     // then); the count's return is read only here, long after it was issued, as the counts of all workgroups go to one
     // word and come back one after another
@@ -536,7 +657,8 @@ size_t moe_attn_workspace_bytes(int n_q_heads, int head_dim, int S) {
     if (n_q_heads < 1 || head_dim != kD || S < 1 || S > kP * kMaxC) return 0;
     const size_t C = (size_t)(S + kP - 1) / kP;
     const size_t scores = ((size_t)n_q_heads * S * sizeof(float) + 255) / 256 * 256;
-    return kHdrBytes + scores + (size_t)n_q_heads * C * 2 * 8 + (size_t)n_q_heads * C * kD * 8;
+    // header, scores, tagged statistics, tagged partials, tagged outputs (read by the folded o projection)
+    return kHdrBytes + scores + (size_t)n_q_heads * C * 2 * 8 + (size_t)n_q_heads * C * kD * 8 + (size_t)n_q_heads * kD * 8;
 }
 
 const char* moe_attn_last_error(void) { return t_err; }
@@ -570,9 +692,9 @@ struct KernelInfo {
 std::mutex g_info_mu;
 std::unordered_map<int, KernelInfo> g_info;
 
-template <int G>
+template <int G, bool OPROJ>
 hipError_t attn_go(FusedAttn& a, hipStream_t st) {
-    const void* fn = reinterpret_cast<const void*>(&attn_fused_kernel<G>);
+    const void* fn = reinterpret_cast<const void*>(&attn_fused_kernel<G, OPROJ>);
     const size_t lds = sizeof(AttnLds<G>);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -580,7 +702,7 @@ hipError_t attn_go(FusedAttn& a, hipStream_t st) {
     KernelInfo info;
     {
         std::lock_guard<std::mutex> lock(g_info_mu);
-        KernelInfo& ki = g_info[dev * 16 + G];
+        KernelInfo& ki = g_info[dev * 32 + 2 * G + (OPROJ ? 1 : 0)];
         if (!ki.ready) {
             ki.err = moe::raise_lds_limit(fn, lds);
             int per_cu = 0, cus = 0;
@@ -598,7 +720,10 @@ hipError_t attn_go(FusedAttn& a, hipStream_t st) {
     if (info.resident > 0)
         while ((size_t)((a.C + a.R - 1) / a.R) * a.NKV > (size_t)info.resident && a.R < a.C) ++a.R;
     a.W = (a.C + a.R - 1) / a.R;
-    hipLaunchKernelGGL(attn_fused_kernel<G>, dim3(a.W, a.NKV), dim3(kT), lds, st, a);
+    a.Wa = a.W * a.NKV;  // workgroup b < Wa: kv head b / W, chunk group b % W
+    int grid = a.Wa;
+    if (OPROJ) grid = std::max(grid, (a.Mo + kORows - 1) / kORows);
+    hipLaunchKernelGGL((attn_fused_kernel<G, OPROJ>), dim3(grid), dim3(kT), lds, st, a);
     return hipGetLastError();
 }
 
@@ -608,13 +733,18 @@ hipError_t attn_go(FusedAttn& a, hipStream_t st) {
 // cleared on this device, which this call then does first.
 int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
                 const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, void* workspace, size_t workspace_bytes,
-                void* stream, bool* cleared) {
+                void* stream, bool* cleared, const uint16_t* wo = nullptr, int o_rows = 0, uint16_t* o_out = nullptr) {
     if (head_dim != kD) return afail(MOE_GPU_EINVAL, "head_dim must be 128");
     const int G = n_kv_heads >= 1 && n_q_heads % n_kv_heads == 0 ? n_q_heads / n_kv_heads : 0;
     if (G != 1 && G != 2 && G != 4 && G != 8)
         return afail(MOE_GPU_EINVAL, "need n_q_heads = G * n_kv_heads with G in {1, 2, 4, 8}");
     if (S < 1 || S > kP * kMaxC) return afail(MOE_GPU_EINVAL, "S outside [1, 65536]");
     if (!q || !k_cache || !v_cache || !out || !workspace) return afail(MOE_GPU_EINVAL, "null pointer");
+    if (wo) {
+        if (n_q_heads * head_dim != kOK) return afail(MOE_GPU_EINVAL, "the folded o projection needs n_q_heads * 128 = 4096");
+        if (o_rows < 1 || !o_out) return afail(MOE_GPU_EINVAL, "o projection: o_rows < 1 or null o_out");
+        if (reinterpret_cast<uintptr_t>(wo) & 15) return afail(MOE_GPU_EINVAL, "w_o must be 16-byte aligned");
+    }
     if (workspace_bytes < moe_attn_workspace_bytes(n_q_heads, head_dim, S))
         return afail(MOE_GPU_EINVAL, "workspace smaller than moe_attn_workspace_bytes()");
     if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
@@ -634,6 +764,10 @@ int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale,
     a.scores = reinterpret_cast<float*>(ws + kHdrBytes);
     a.stats = reinterpret_cast<uint64_t*>(ws + kHdrBytes + scores_bytes);
     a.part = a.stats + (size_t)n_q_heads * C * 2;
+    a.aout = a.part + (size_t)n_q_heads * C * kD;
+    a.wo = wo;
+    a.o_out = o_out;
+    a.Mo = o_rows;
     a.NQ = n_q_heads;
     a.NKV = n_kv_heads;
     a.S = S;
@@ -650,11 +784,20 @@ int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale,
         }
     }
     hipError_t e = hipSuccess;
-    switch (G) {
-        case 1: e = attn_go<1>(a, st); break;
-        case 2: e = attn_go<2>(a, st); break;
-        case 4: e = attn_go<4>(a, st); break;
-        default: e = attn_go<8>(a, st); break;
+    if (wo) {
+        switch (G) {
+            case 1: e = attn_go<1, true>(a, st); break;
+            case 2: e = attn_go<2, true>(a, st); break;
+            case 4: e = attn_go<4, true>(a, st); break;
+            default: e = attn_go<8, true>(a, st); break;
+        }
+    } else {
+        switch (G) {
+            case 1: e = attn_go<1, false>(a, st); break;
+            case 2: e = attn_go<2, false>(a, st); break;
+            case 4: e = attn_go<4, false>(a, st); break;
+            default: e = attn_go<8, false>(a, st); break;
+        }
     }
     if (e != hipSuccess) return afail(e == hipErrorNoBinaryForGpu ? MOE_GPU_ENOKERNEL : MOE_GPU_EHIP, hipGetErrorString(e));
     return MOE_GPU_OK;
@@ -666,7 +809,7 @@ int attn_launch(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale,
 // current) and kept in g_scratch; g_scratch_clear records that the first call on the device cleared it.
 constexpr int kScratchMaxNQ = 64, kScratchMaxS = 8192;
 constexpr size_t kScratchBytes = kHdrBytes + (size_t)kScratchMaxNQ * kScratchMaxS * sizeof(float) +
-                                 (size_t)kScratchMaxNQ * (kScratchMaxS / kP) * (2 + kD) * 8;
+                                 (size_t)kScratchMaxNQ * (kScratchMaxS / kP) * (2 + kD) * 8 + (size_t)kScratchMaxNQ * kD * 8;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 constexpr int kMaxDevices = 64;
 void* g_scratch[kMaxDevices];
@@ -700,6 +843,14 @@ int moe_attn_decode_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, floa
                         size_t workspace_bytes, void* stream) {
     return attn_launch(n_q_heads, n_kv_heads, head_dim, S, scale, q, k_cache, v_cache, out, workspace, workspace_bytes,
                        stream, nullptr);
+}
+
+int moe_attn_decode_oproj_dev(int n_q_heads, int n_kv_heads, int head_dim, int S, float scale, const uint16_t* q,
+                              const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out, const uint16_t* w_o,
+                              int o_rows, uint16_t* o_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!w_o) return afail(MOE_GPU_EINVAL, "null w_o");
+    return attn_launch(n_q_heads, n_kv_heads, head_dim, S, scale, q, k_cache, v_cache, out, workspace, workspace_bytes,
+                       stream, nullptr, w_o, o_rows, o_out);
 }
 
 size_t moe_attn_noalloc_max_bytes(void) { return kScratchBytes; }

@@ -5,8 +5,8 @@
 //   h  = rmsnorm(x, input_layernorm)                       folded into the q|k|v GEMV (moe_qkv_rope_append_dev)
 //   q, k, v = round_bf(gemv(q|k|v_proj, h))                one [QD + 2 KVD, H] table, one launch, whose epilogue
 //   rope(q), rope(k), kc[pos] = k, vc[pos] = v             ropes q and k and appends k and v to the caches
-//   a  = attention(q, kc[0..pos], vc[0..pos])              moe_attn_decode_dev
-//   o  = round_bf(gemv(o_proj, a))                         moe_gemv_dev
+//   a  = attention(q, kc[0..pos], vc[0..pos])              moe_attn_decode_oproj_dev (one launch for both when
+//   o  = round_bf(gemv(o_proj, a))                         QD = 4096; else moe_attn_decode_dev + moe_gemv_dev)
 //   x  = bf16(x + o); h2 = rmsnorm(x, post_attention_layernorm); x = bf16(x + bf16(bf16(moe) + bf16(shared)))
 //                                                          one fused MoE launch (moe_gpu_block_dev)
 // and after the last layer the final RMSNorm, the LM-head GEMV and the greedy argmax (moe_head_argmax_dev).  Every
@@ -140,10 +140,17 @@ int run_step(moe_model* m, const int32_t* token, int pos, int32_t* next, float* 
         SUB(m, moe_qkv_rope_append_dev(c.H, c.n_q_heads, c.n_kv_heads, c.head_dim, m->qkv_w[l], x, m->in_norm[l], c.eps,
                                        cs, sn, m->qkv, m->kc[l], m->vc[l], pos, m->stream),
             "q|k|v projection, rope, kv append");
-        SUB(m, moe_attn_decode_dev(c.n_q_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->qkv, m->kc[l], m->vc[l],
-                                   m->attn, m->attn_ws, m->attn_ws_bytes, m->stream),
-            "attention");
-        SUB(m, moe_gemv_dev(c.H, m->QD, m->o_w[l], m->attn, m->o, m->stream), "o projection");
+        if (m->QD == 4096) {  // attention and the o projection in one launch (its weights stream during the exchanges)
+            SUB(m, moe_attn_decode_oproj_dev(c.n_q_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->qkv, m->kc[l],
+                                             m->vc[l], m->attn, m->o_w[l], c.H, m->o, m->attn_ws, m->attn_ws_bytes,
+                                             m->stream),
+                "attention + o projection");
+        } else {
+            SUB(m, moe_attn_decode_dev(c.n_q_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->qkv, m->kc[l],
+                                       m->vc[l], m->attn, m->attn_ws, m->attn_ws_bytes, m->stream),
+                "attention");
+            SUB(m, moe_gemv_dev(c.H, m->QD, m->o_w[l], m->attn, m->o, m->stream), "o projection");
+        }
         SUB(m, moe_gpu_block_dev(m->experts, l, 1, x, m->o, m->post_norm[l], c.eps, 0, 0, xn, nullptr, nullptr,
                                  nullptr),
             "moe block");

@@ -41,7 +41,7 @@ SYMBOLS = (
     "moe_rmsnorm_dev", "moe_gemv_dev", "moe_gemv_f32_dev", "moe_gemv_norm_dev", "moe_rope_dev", "moe_rope_append_dev",
     "moe_qkv_rope_append_dev",
     "moe_attn_workspace_bytes", "moe_attn_decode_dev", "moe_attn_last_error", "moe_attn_noalloc_max_bytes",
-    "moe_attn_decode_noalloc_dev",
+    "moe_attn_decode_noalloc_dev", "moe_attn_decode_oproj_dev",
     "moe_gpu_block_dev",
     "moe_model_create", "moe_model_destroy", "moe_model_last_error", "moe_model_experts", "moe_model_head",
     "moe_model_set_stream", "moe_model_synchronize", "moe_model_load_layer", "moe_model_load_embedding",
@@ -148,6 +148,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "moe_attn_last_error": (C.c_char_p, []),
         "moe_attn_noalloc_max_bytes": (C.c_size_t, []),
         "moe_attn_decode_noalloc_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp]),
+        "moe_attn_decode_oproj_dev": (i, [i, i, i, i, f, vp, vp, vp, vp, vp, i, vp, vp, C.c_size_t, vp]),
         "moe_gemv_norm_dev": (i, [i, i, vp, vp, vp, f, vp, vp]),
         "moe_gemv_f32_dev": (i, [i, i, vp, vp, vp, vp]),
         "moe_rope_append_dev": (i, [i, i, i, vp, vp, vp, vp, vp, i, vp]),
@@ -513,6 +514,21 @@ def attn_decode_dev(q, k_cache, v_cache, out, workspace, n_q_heads: int, n_kv_he
     ws_bytes = workspace.numel() * workspace.element_size()
     rc = L.moe_attn_decode_dev(n_q_heads, n_kv_heads, head_dim, S, scale, _p(q), _p(k_cache), _p(v_cache), _p(out),
                                _p(workspace), ws_bytes, getattr(stream, "cuda_stream", stream))
+    if rc != OK:
+        raise MoeGpuError(rc, L.moe_attn_last_error().decode())
+
+
+def attn_decode_oproj_dev(q, k_cache, v_cache, out, w_o, o_out, workspace, n_q_heads: int, n_kv_heads: int, S: int,
+                          scale: float | None = None, head_dim: int = 128, stream=None) -> None:
+    """attn_decode_dev with the o projection in the same launch (main.rs:86-104, :119): out as attn_decode_dev and
+    o_out [M] = bf16(w_o . out), w_o [M, NQ * D] bf16 bits (NQ * D = 4096), bit-identical to gemv_dev(w_o, out)."""
+    L = load_library()
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = L.moe_attn_decode_oproj_dev(n_q_heads, n_kv_heads, head_dim, S, scale, _p(q), _p(k_cache), _p(v_cache),
+                                     _p(out), _p(w_o), int(w_o.shape[0]), _p(o_out), _p(workspace), ws_bytes,
+                                     getattr(stream, "cuda_stream", stream))
     if rc != OK:
         raise MoeGpuError(rc, L.moe_attn_last_error().decode())
 

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from moe_gpu import EINVAL, MoeGpuError, attn_decode_dev, attn_scores, attn_workspace_bytes
+from moe_gpu import (EINVAL, MoeGpuError, attn_decode_dev, attn_decode_oproj_dev, attn_scores, attn_workspace_bytes,
+                     gemv_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -153,3 +154,56 @@ def test_attention_errors():
         with pytest.raises(MoeGpuError) as e:
             attn_decode_dev(x, x, x, x, ws, NQ, NKV, S, head_dim=D)
         assert e.value.code == EINVAL
+
+
+@pytest.mark.parametrize("NQ,NKV,S,M", [(32, 8, 4096, 4096), (32, 8, 1, 4096), (32, 8, 300, 4096), (32, 4, 777, 4096),
+                                        (32, 16, 513, 4096), (32, 8, 9000, 4096), (32, 8, 1000, 1000)])
+def test_attention_oproj_matches_two_launches(NQ, NKV, S, M, monkeypatch):
+    """The o projection folded into the attention launch (moe_attn_decode_oproj_dev) against attention then the
+    dense GEMV (moe_attn_decode_dev + moe_gemv_dev) on the same inputs: out and o bit for bit, also with every wait
+    ended at once (MOE_ATTN_POLL=0: the attention outputs recomputed by each workgroup)."""
+    import torch
+
+    say(f"attention + o projection NQ={NQ} NKV={NKV} S={S} M={M}")
+    dev = "cuda:0"
+    rng = np.random.default_rng(S + NKV + M)
+    q = O.f2bf(rng.standard_normal((NQ, 128)).astype(np.float32))
+    k = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    v = O.f2bf(rng.standard_normal((S, NKV, 128)).astype(np.float32))
+    wo = O.f2bf((0.02 * rng.standard_normal((M, NQ * 128))).astype(np.float32))
+    qd, kd, vd, wod = (torch.from_numpy(a.view(np.int16)).to(dev) for a in (q, k, v, wo))
+    ws = torch.zeros(attn_workspace_bytes(NQ, S) // 4, dtype=torch.float32, device=dev)
+    a1 = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    o1 = torch.zeros(M, dtype=torch.int16, device=dev)
+    torch.cuda.synchronize()
+    attn_decode_dev(qd, kd, vd, a1, ws, NQ, NKV, S)
+    gemv_dev(wod, a1.view(-1), o1)
+    torch.cuda.synchronize()
+    for poll in (None, "0"):
+        if poll is not None:
+            monkeypatch.setenv("MOE_ATTN_POLL", poll)
+        a2 = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+        o2 = torch.zeros(M, dtype=torch.int16, device=dev)
+        for _ in range(2):  # twice: the second call's epoch differs, no stale words are taken
+            attn_decode_oproj_dev(qd, kd, vd, a2, wod, o2, ws, NQ, NKV, S)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(a2.cpu().numpy(), a1.cpu().numpy())
+        np.testing.assert_array_equal(o2.cpu().numpy(), o1.cpu().numpy())
+    monkeypatch.delenv("MOE_ATTN_POLL")
+    ref, _ = O.attention(q, k, v, NKV)
+    check_out(a1.cpu().numpy().view(np.uint16), ref)
+
+
+def test_attention_oproj_errors():
+    import torch
+
+    dev = "cuda:0"
+    NQ, NKV, S = 16, 4, 64  # NQ * 128 = 2048: the folded projection needs 4096 columns
+    q = torch.zeros((NQ, 128), dtype=torch.int16, device=dev)
+    k = torch.zeros((S, NKV, 128), dtype=torch.int16, device=dev)
+    ws = torch.zeros(attn_workspace_bytes(NQ, S) // 4, dtype=torch.float32, device=dev)
+    wo = torch.zeros((4096, NQ * 128), dtype=torch.int16, device=dev)
+    o = torch.zeros(4096, dtype=torch.int16, device=dev)
+    with pytest.raises(MoeGpuError) as ei:
+        attn_decode_oproj_dev(q, k, k, q, wo, o, ws, NQ, NKV, S)
+    assert ei.value.code == EINVAL
