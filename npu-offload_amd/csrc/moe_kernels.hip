@@ -47,6 +47,10 @@ typedef LDS_AS float lds_float;
 constexpr unsigned kSpinLimit = 1u << 20;  // bounded dependency waits (~1 s): a wait never hangs the GPU
 // Shared-memory scratch of route_local (carved from the act-row region, unused while a unit computes its routing).
 constexpr int kRouteKeys = 1024;  // sort keys of one pass (tokens x experts)
+#ifndef MOE_TOPK_THREADS
+#define MOE_TOPK_THREADS 512
+#endif
+constexpr int kTopkThreads = MOE_TOPK_THREADS;  // the standalone routing kernel's workgroup
 constexpr size_t kRouteScratchBytes = (size_t)kRouteKeys * 8 + (size_t)kRouteKeys * 4;
 
 __device__ __forceinline__ float bf_lo(unsigned v) { return __uint_as_float(v << 16); }
@@ -638,9 +642,9 @@ __device__ __forceinline__ float sigmoid_ref(float v) {
     return 1.f / (1.f + ex);
 }
 
-// The largest of the wave's 64-bit keys, in every lane: DPP moves within rows of 16 lanes (each step combining equal
-// halves), then the four rows' maxima.  All 64 lanes must be active.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+// The largest of each 16-lane row's 64-bit keys, in every lane of the row (DPP moves within the row, each step
+// combining equal halves).  All 64 lanes must be active.
+__device__ __forceinline__ uint64_t row_max_u64(uint64_t v) {
 #define MOE_DPP_MAX_STEP(CTRL)                                                                             \
     {                                                                                                      \
         const unsigned lo_ = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)v, CTRL, 0xF, 0xF, false);  \
@@ -653,15 +657,40 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     MOE_DPP_MAX_STEP(0x141)  // row half mirror
     MOE_DPP_MAX_STEP(0x140)  // row mirror
 #undef MOE_DPP_MAX_STEP
-    uint64_t m = 0;
+    return v;
+}
+
+// Several tokens' selection: token tl of the pass (t0 + tl overall) on row tl of the workgroup's 16-lane rows, KQ keys
+// per lane (experts l, l + 16, .. of the token's E), k rounds of the row maximum.  Called by the whole workgroup.
+template <int KQ>
+__device__ __forceinline__ void select_rows(lds_RouteTab* rt, const LDS_AS uint64_t* keys, const LDS_AS float* sgv,
+                                            int t0, int nt, int E, int k, int rule) {
+    const int g = threadIdx.x >> 4, l16 = threadIdx.x & 15, ng = blockDim.x >> 4;
+    for (int base = 0; base < nt; base += ng) {  // uniform: every lane runs the DPP steps
+        const int tl = base + g;
+        const bool live = tl < nt;
+        uint64_t kk[KQ];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 16 * r);
-        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 16 * r);
-        const uint64_t x = ((uint64_t)hi << 32) | lo;
-        m = x > m ? x : m;
+        for (int q = 0; q < KQ; q++) kk[q] = live && l16 + 16 * q < E ? keys[tl * E + l16 + 16 * q] : 0ull;
+        for (int r = 0; r < k; r++) {
+            uint64_t m[KQ];
+#pragma unroll
+            for (int q = 0; q < KQ; q++) m[q] = kk[q];
+#pragma unroll
+            for (int w = KQ / 2; w >= 1; w >>= 1)
+#pragma unroll
+                for (int q = 0; q < w; q++) m[q] = m[q + w] > m[q] ? m[q + w] : m[q];
+            const uint64_t top = row_max_u64(m[0]);
+#pragma unroll
+            for (int q = 0; q < KQ; q++)
+                if (kk[q] == top) kk[q] = 0ull;
+            if (live && l16 == 0) {
+                const int t = t0 + tl, e = (int)~(unsigned)top;
+                rt->id[t * k + r] = e;
+                rt->gate[t * k + r] = rule == kRouteSigmoid ? sgv[tl * E + e] : route_key_score(top);
+            }
+        }
     }
-    return m;
 }
 
 // Top-k and expert grouping into rt.  Selection: the k largest keys (score descending, index ascending); each thread
@@ -727,30 +756,13 @@ __device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned cha
                 }
             }
             __syncthreads();
-            if (MULTI && T > 1 && E <= 4 * 64) {
-                // 2'. several tokens: one wavefront per token takes the k largest keys one by one (a key's expert index
-                //     makes every key distinct, so this is the same selection as counting ranks below), lane l holding
-                //     the keys of experts l, l + 64, ...; the taken key is zeroed (every real key is nonzero)
-                const int wave = wave_id(), lane = tid & 63;
-                for (int tl = wave; tl < nt; tl += nthr / 64) {
-                    const int t = t0 + tl;
-                    uint64_t kk[4];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) kk[q] = lane + 64 * q < E ? keys[tl * E + lane + 64 * q] : 0ull;
-                    for (int r = 0; r < k; r++) {
-                        const uint64_t best = max(max(kk[0], kk[1]), max(kk[2], kk[3]));
-                        const uint64_t top = wave_max_u64(best);
-                        const int e = (int)~(unsigned)top;
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            if (kk[q] == top) kk[q] = 0ull;
-                        if (lane == 0) {
-                            rt->id[t * k + r] = e;
-                            rt->gate[t * k + r] =
-                                rule == kRouteSigmoid ? ((const LDS_AS float*)cnt)[tl * E + e] : route_key_score(top);
-                        }
-                    }
-                }
+            if (MULTI && T > 1 && E <= 16 * 16) {
+                // 2'. several tokens: one 16-lane row per token takes the k largest keys one by one (a key's expert
+                //     index makes every key distinct, so this is the same selection as counting ranks below), lane l of
+                //     the row holding the keys of experts l, l + 16, ...; the row's maximum takes four DPP moves and no
+                //     cross-row step, and the taken key is zeroed (every real key is nonzero)
+                if (E <= 8 * 16) select_rows<8>(rt, keys, (const LDS_AS float*)cnt, t0, nt, E, k, rule);
+                else select_rows<16>(rt, keys, (const LDS_AS float*)cnt, t0, nt, E, k, rule);
                 __syncthreads();
             } else {
             // 2. ranks: work item (part p, item i) counts the keys of experts [p E / parts, (p + 1) E / parts) above
@@ -847,59 +859,102 @@ __device__ __forceinline__ int route_local(lds_RouteTab* rt, LDS_AS unsigned cha
         return 0;
     }
     bad = __syncthreads_or(bad);
-    // Grouping: thread p owns entry p = t * keep + r (n = T * keep <= 128); entries are compared through shared-memory
-    // broadcasts.  A slot's number counts the first occurrences before its own first occurrence.
+    // Grouping: entry p = t * keep + r (n = T * keep <= 128).  A slot's number counts the first occurrences before its
+    // own first occurrence.
     const int n = T * keep;
-    LDS_AS int* ent = (LDS_AS int*)scr;  // entry -> expert, padded with -2 to a multiple of 4
-    LDS_AS int* fst = ent + 128;         // 1 where an entry is its expert's first occurrence
-    const int n4 = (n + 3) & ~3;
-    int my_e = -1, first = 0, pos = 0, c = 0;
-    if (tid < n4) {
-        my_e = tid < n ? rt->id[(tid / keep) * k + tid % keep] : -2;
-        ent[tid] = my_e;
-    }
-    __syncthreads();
-    if (tid < n && my_e >= 0) {
-        first = tid;
-        for (int j = 0; j < n4; j += 4) {
-            const i32x4 q = *(const LDS_AS i32x4*)(ent + j);
-            const int v[4] = {q.x, q.y, q.z, q.w};
+    if (MULTI && do_topk) {
+        // The selection's entries: distinct experts within a token, every id in [0, E).  Per expert, the tokens that
+        // hold it (a bit mask) and its first entry, by shared-memory atomics; first occurrences are counted from two
+        // wave ballots.
+        LDS_AS unsigned* tmask = (LDS_AS unsigned*)scr;
+        LDS_AS unsigned* firstp = tmask + kMaxExperts;
+        LDS_AS uint64_t* fmask = (LDS_AS uint64_t*)(firstp + kMaxExperts);
+        for (int e = tid; e < E; e += nthr) {
+            tmask[e] = 0u;
+            firstp[e] = ~0u;
+        }
+        __syncthreads();
+        int e = 0, t = 0;
+        if (tid < n) {
+            t = tid / keep;
+            e = rt->id[t * k + tid - t * keep];
+            __hip_atomic_fetch_or(&tmask[e], 1u << t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_min(&firstp[e], (unsigned)tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __syncthreads();
+        const bool isfirst = tid < n && firstp[e] == (unsigned)tid;
+        const uint64_t bm = __ballot(isfirst);
+        if ((tid & 63) == 0 && tid < 128) fmask[tid >> 6] = bm;
+        __syncthreads();
+        const uint64_t m0 = fmask[0], m1 = fmask[1];
+        if (tid < n) {
+            const unsigned f = firstp[e], tm = tmask[e];
+            const int before =
+                f < 64 ? __popcll(m0 & ((1ull << f) - 1)) : __popcll(m0) + __popcll(m1 & ((1ull << (f - 64)) - 1));
+            const int slot = n_shared + before;
+            if (isfirst) {
+                rt->slot_e[slot] = (short)e;
+                rt->slot_n[slot] = (unsigned char)__popc(tm);
+            }
+            rt->slot_p[slot][__popc(tm & ((1u << t) - 1))] = (unsigned char)tid;
+        }
+        if (tid == 0) {
+            rt->nslot = n_shared + __popcll(m0) + __popcll(m1);
+            rt->err = bad;
+        }
+    } else {
+        // The caller's entries (ids may repeat within a token): compared through shared-memory broadcasts.
+        LDS_AS int* ent = (LDS_AS int*)scr;  // entry -> expert, padded with -2 to a multiple of 4
+        LDS_AS int* fst = ent + 128;         // 1 where an entry is its expert's first occurrence
+        const int n4 = (n + 3) & ~3;
+        int my_e = -1, first = 0, pos = 0, c = 0;
+        if (tid < n4) {
+            my_e = tid < n ? rt->id[(tid / keep) * k + tid % keep] : -2;
+            ent[tid] = my_e;
+        }
+        __syncthreads();
+        if (tid < n && my_e >= 0) {
+            first = tid;
+            for (int j = 0; j < n4; j += 4) {
+                const i32x4 q = *(const LDS_AS i32x4*)(ent + j);
+                const int v[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const bool hit = v[u] == my_e;
-                c += hit;
-                pos += hit && j + u < tid;
-                if (hit && j + u < first) first = j + u;
+                for (int u = 0; u < 4; u++) {
+                    const bool hit = v[u] == my_e;
+                    c += hit;
+                    pos += hit && j + u < tid;
+                    if (hit && j + u < first) first = j + u;
+                }
             }
         }
-    }
-    if (tid < n4) fst[tid] = tid < n && my_e >= 0 && first == tid;
-    __syncthreads();
-    int rep = 0;
-    int before = 0;  // first occurrences before mine: a uniform loop over all entries
-    for (int j = 0; j < n4; j += 4) {
-        const i32x4 q = *(const LDS_AS i32x4*)(fst + j);
-        before += (j < first ? q.x : 0) + (j + 1 < first ? q.y : 0) + (j + 2 < first ? q.z : 0) +
-                  (j + 3 < first ? q.w : 0);
-    }
-    if (tid < n && my_e >= 0) {
-        const int slot = n_shared + before;
-        if (first == tid) {
-            rt->slot_e[slot] = (short)my_e;
-            rt->slot_n[slot] = (unsigned char)(c < T ? c : T);
+        if (tid < n4) fst[tid] = tid < n && my_e >= 0 && first == tid;
+        __syncthreads();
+        int rep = 0;
+        int before = 0;  // first occurrences before mine: a uniform loop over all entries
+        for (int j = 0; j < n4; j += 4) {
+            const i32x4 q = *(const LDS_AS i32x4*)(fst + j);
+            before += (j < first ? q.x : 0) + (j + 1 < first ? q.y : 0) + (j + 2 < first ? q.z : 0) +
+                      (j + 3 < first ? q.w : 0);
         }
-        if (pos < T) {
-            rt->slot_p[slot][pos] = (unsigned char)tid;
-        } else {  // an expert repeated within one token's ids: the extra entry is dropped
-            rt->id[(tid / keep) * k + tid % keep] = -1;
-            rep = 1;
+        if (tid < n && my_e >= 0) {
+            const int slot = n_shared + before;
+            if (first == tid) {
+                rt->slot_e[slot] = (short)my_e;
+                rt->slot_n[slot] = (unsigned char)(c < T ? c : T);
+            }
+            if (pos < T) {
+                rt->slot_p[slot][pos] = (unsigned char)tid;
+            } else {  // an expert repeated within one token's ids: the extra entry is dropped
+                rt->id[(tid / keep) * k + tid % keep] = -1;
+                rep = 1;
+            }
         }
-    }
-    const int nfirst = __syncthreads_count(tid < n && my_e >= 0 && first == tid);
-    rep = __syncthreads_or(rep);
-    if (tid == 0) {
-        rt->nslot = n_shared + nfirst;
-        rt->err = rep ? 2 : bad;
+        const int nfirst = __syncthreads_count(tid < n && my_e >= 0 && first == tid);
+        rep = __syncthreads_or(rep);
+        if (tid == 0) {
+            rt->nslot = n_shared + nfirst;
+            rt->err = rep ? 2 : bad;
+        }
     }
     if (tid < n_shared) {
         rt->slot_e[tid] = (short)(-1 - tid);
@@ -1345,7 +1400,7 @@ __global__ __launch_bounds__(256) void router_kernel(LayerPtrs L, Dims d, int T,
     else router_unit<kRouterTG>(s, L.wr, e0, d.E, d.H, T, logits, logits_out, epoch, true, in, false, u0, u1, t0);
 }
 
-__global__ __launch_bounds__(256) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
+__global__ __launch_bounds__(kTopkThreads) void topk_group_kernel(LayerPtrs L, Dims d, int T, int keep, int n_shared,
                                                          int do_topk, int rule, const uint64_t* __restrict__ logits,
                                                          unsigned epoch, unsigned* err, int32_t* __restrict__ ids,
                                                          float* __restrict__ gates, Slots* __restrict__ slots) {
@@ -1824,7 +1879,7 @@ hipError_t launch_router(const LayerPtrs& L, const Dims& d, int T, const StageSr
 hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep, int n_shared, bool do_topk, int rule,
                              const uint64_t* logits, unsigned epoch, unsigned* err, int32_t* ids, float* gates,
                              Slots* slots, hipStream_t st) {
-    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(256), 0, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, rule,
+    hipLaunchKernelGGL(topk_group_kernel, dim3(1), dim3(kTopkThreads), 0, st, L, d, T, keep, n_shared, do_topk ? 1 : 0, rule,
                        logits, epoch, err, ids, gates, slots);
     return hipGetLastError();
 }
