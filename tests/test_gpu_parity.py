@@ -56,6 +56,40 @@ def test_tiny_route_bitexact(tiny):
         check_route(ids, gates, ref, TINY.k)
 
 
+# ------------------------------------------------------------------------- several-token routing, wide expert counts
+# The several-token selection has three layouts (E <= 128: up to 8 keys per lane of a token's 16-lane row; E <= 256: up
+# to 16; above: rank counting, several passes of 1024 keys), and the grouping counts first occurrences over two
+# 64-entry ballots (T * keep up to 128 entries).  Batch 16 runs the standalone routing kernel, batch 5 the fused
+# kernel's per-workgroup routing.
+WIDE = [Workload("wide: H=1024 E=200+1 shared top-8 F=256", 1024, 256, 200, 8, 1, zipf_s=1.1, seed=31),
+        Workload("wide: H=1024 E=300 top-6 F=256", 1024, 256, 300, 6, 0, zipf_s=1.1, seed=32)]
+
+
+@pytest.mark.parametrize("wi", [0, 1])
+def test_route_and_layer_many_tokens_wide_experts(wi):
+    w = WIDE[wi]
+    say(f"{w.name}: upload numpy-normal weights")
+    rng = np.random.default_rng(40 + wi)
+    hl = random_layer(w, rng)
+    tier = MoeGpu(w.H, w.F, w.E, w.k, w.n_shared, n_layers=1, max_tokens=16)
+    try:
+        upload(tier, hl)
+        for T in (16, 5):
+            x = random_x(T, w.H, rng)
+            for keep in (w.k, w.k // 2):
+                say(f"  T={T} keep={keep}: route, then the layer")
+                ids, gates, lg = tier.route(0, x, keep=keep, want_logits=True)
+                ref = oracle_layer(hl, x, keep=keep)
+                np.testing.assert_array_equal(lg.view(np.uint32), ref["logits"].view(np.uint32))
+                check_route(ids, gates, ref, keep)
+                out, ids2, gates2 = tier.layer(0, x, keep=keep)
+                np.testing.assert_array_equal(ids2, ids)
+                np.testing.assert_array_equal(gates2.view(np.uint32), gates.view(np.uint32))
+                assert_layer_close(out, ref["out"])
+    finally:
+        tier.close()
+
+
 def test_tiny_layer(tiny):
     tier, hl = tiny
     rng = np.random.default_rng(2)
