@@ -546,7 +546,7 @@ def bench_decode(args) -> None:
         "config": {"workload": "decode: 48 layers x (RMSNorm + GQA attention 32q/8kv d128 over KV 4096 + RMSNorm + "
                                "Solar MoE block H4096 F1280 E128+1 top-8) + LM head V196608, greedy, batch 1",
                    "layers": L, "kv_len": DEC_CTX, "vocab": V, "tokens": 1},
-        "roofline": {"kernel": "whole step (4 launches per layer + head)", "bound": "hbm", "achieved": round(achieved, 1),
+        "roofline": {"kernel": "whole step (3 launches per layer, 3 more per token)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                      "bytes_per_launch": int(nbytes), "avg_us": round(ev_s / K * 1e6, 1),
                      "timing": "timed-region hipEvents on the model's stream over K chained steps"},
