@@ -1414,10 +1414,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_group_kernel(LayerPtrs L, D
 
 #endif  // MOE_COMMON
 
+// The unfused gate|up kernel's shared memory: the staged tokens and the cross-wave reduction only (its units read no
+// act rows), so that two workgroups fit on a CU at batch 8 (2 x 72 KiB).
+__host__ __device__ inline size_t gu_lds_bytes(int T, int NT, int H) {
+    return (size_t)T * (H / 8) * 16 + (size_t)4 * NT * 64 * 4;
+}
+
 template <int NT>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a, Sync* sy) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    const Lds s = lds_carve(lds_raw, a.T, NT, a.d.H, a.d.F, a.d.E);
+    Lds s;
+    s.xs = (lds_u32x4*)(LDS_AS unsigned char*)lds_raw;
+    s.as = nullptr;
+    s.red = (lds_float*)((LDS_AS unsigned char*)lds_raw + (size_t)a.T * (a.d.H / 8) * 16);
+    s.xf = nullptr;
     if (blockIdx.x == 0 && threadIdx.x < 2) st_sync(&sy->next_unit[threadIdx.x * kSyncPad], 0u);  // fused queue heads
     const int ntile = a.d.F / 32, S = a.d.n_shared, gs = ntile * a.kps, g = ntile * a.kp;
     const int b = (int)blockIdx.x, shared = b < S * gs;  // shared slots' parts first
@@ -1889,7 +1899,7 @@ hipError_t launch_topk_group(const LayerPtrs& L, const Dims& d, int T, int keep,
 template <int NT>
 hipError_t gateup_nt(const ExpertArgs& ea, Sync* sy, hipStream_t st) {
     const int maxs = ea.maxs;
-    const size_t lds = lds_bytes(ea.T, NT, ea.d.H, ea.d.F, ea.d.E);
+    const size_t lds = gu_lds_bytes(ea.T, NT, ea.d.H);
     hipError_t e = set_lds(reinterpret_cast<const void*>(&gateup_kernel<NT>), lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gateup_kernel<NT>, dim3(gateup_units(maxs, ea.d.n_shared, ea.d.F, ea.kp, ea.kps)), dim3(256), lds, st, ea, sy);
